@@ -1,0 +1,225 @@
+"""Benchmark of the reproducible FP32 GEMM on one MI355X.
+
+Workload (the 4096^3 case the headline metric is quoted on):
+C = A B, M = N = K = 4096, S = 3 slices, no transposes, adversarial dynamic range inputs
+(random signs, |x| = 2^e with e ~ U[-60, 60], 5% zeros, 1% subnormals, near-negative
+pairs along k). A "step" is one full reproducible GEMM: slice split of both operands,
+int8 MFMA contraction, exact recombination and rounding, with inputs resident in HBM.
+
+Prints one JSON line: effective FP32 TFLOP/s = 2 M N K / time (the reference's definition,
+repro_gemm_cuda/bench_repro_gemm.cu:72-75), the contraction kernel's int8 rate against the
+MI355X dense int8 MFMA peak (measured with HIP events on the launch stream), whether the
+output bits equal the CPU reference's, and the reference CPU path timed on this host.
+
+  python bench.py [--steps K] [--warmup W] [--no-cpu] [--size N]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
+FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
+
+# --------------------------------------------------------------------------------------
+# Synthetic input (same recipe and bits as tests/golden/configs.py config 4), vectorised
+# SplitMix64 in numpy: draw i of seed s is mix(s + (i + 1) * gamma).
+# --------------------------------------------------------------------------------------
+_G = np.uint64(0x9E3779B97F4A7C15)
+
+
+def _draw(seed, idx):
+    z = np.uint64(seed) + (idx + np.uint64(1)) * _G
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def _adversarial(rows, cols, seed, pair_rows, negate):
+    r = np.arange(rows, dtype=np.uint64)[:, None]
+    c = np.arange(cols, dtype=np.uint64)[None, :]
+    one = np.uint64(1)
+    if pair_rows:
+        base = (r & ~one) * np.uint64(cols) + c
+        second = np.broadcast_to((r & one) == one, (rows, cols))
+    else:
+        base = r * np.uint64(cols) + (c & ~one)
+        second = np.broadcast_to((c & one) == one, (rows, cols))
+    u = _draw(seed, np.uint64(2) * base)
+    v = _draw(seed, np.uint64(2) * base + one)
+    pct = u % np.uint64(100)
+    sign = ((v >> np.uint64(63)) & one).astype(np.uint32) << np.uint32(31)
+    f = ((v >> np.uint64(8)) & np.uint64(0x7FFFFF)).astype(np.uint32)
+    f = np.where(f == 0, np.uint32(1), f)
+    e = ((v >> np.uint64(16)) % np.uint64(121)).astype(np.int64) - 60
+    normal = ((e + 127).astype(np.uint32)) << np.uint32(23)
+    b = np.where(pct < 5, np.uint32(0), np.where(pct < 6, f, normal)) | sign
+    x = b.astype(np.uint32).view(np.float32)
+    w = _draw(np.uint64(seed) ^ np.uint64(0x5BD1E995), base)
+    t = (w % np.uint64(3)).astype(np.int64) - 1
+    fac = (np.float32(1.0) + t.astype(np.float32) * np.float32(1.0 / 1048576.0)).astype(np.float32)
+    y = (x * fac).astype(np.float32)
+    if negate:
+        y = -y
+    return np.where(second, y, x).astype(np.float32)
+
+
+def make_inputs(n):
+    A = _adversarial(n, n, 4001, pair_rows=False, negate=True)
+    B = _adversarial(n, n, 4002, pair_rows=True, negate=False)
+    return np.ascontiguousarray(A), np.ascontiguousarray(B)
+
+
+# --------------------------------------------------------------------------------------
+# CPU baseline: the reference's own CPU path (oracle/_ref) or this repository's port.
+# --------------------------------------------------------------------------------------
+def cpu_baseline(A, B, n, gpu_C, threads, reps):
+    from oracle import oracle as O  # the CPU checker, used only in this leg
+
+    os.environ["REPRO_CPU_THREADS"] = str(threads)
+    kind = "reference" if O.ref is not None else "port"
+    times = []
+    C = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        if kind == "reference":
+            C = O.ref_cpu_gemm(A, B, n, n, n, 0, 0, 3)
+        else:
+            C = O.cpu_gemm(A, B, n, n, n, 0, 0, 3, threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    match = bool(np.array_equal(C.view(np.uint32), gpu_C.view(np.uint32)))
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:  # noqa: BLE001
+        model = "unknown"
+    return {
+        "value": round(2.0 * n * n * n / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": "the full %d^3 S=3 GEMM (same inputs), wall clock incl. quantisation, "
+                  "median of %d; cpu %s; bits equal GPU: %s" % (n, reps, model, match),
+        "ms": round(t * 1e3, 2),
+        "bits_equal_gpu": match,
+        "output_hash": "%016x" % O.fnv1a64(C),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--size", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the reproducible GEMM shards without changing bits; see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import bit_reproducible_training_amd as rg
+
+    n = args.size
+    M = N = K = n
+    S = 3
+    A, B = make_inputs(n)
+    dA = torch.from_numpy(A).cuda()
+    dB = torch.from_numpy(B).cuda()
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    cfg = rg.Config(slices=S)
+    plan = rg.make_plan(M, N, K, cfg)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(events=None):
+        code = rg.repro_gemm_fp32_ws(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), M, N, K, cfg,
+                                     ws.data_ptr(), ws.numel(), sp, events)
+        if code != 0:
+            raise rg.ReproGemmError(code, "bench step")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` GEMMs; stage events on the launch stream give the
+    # contraction kernel's own duration (event 1 -> event 2 brackets only that launch).
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step([e.cuda_event for e in evs[i]])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    slice_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    contract_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    final_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in evs)
+
+    eff_tflops = 2.0 * M * N * K / (ms_per_step * 1e-3) / 1e12
+    int8_ops = S * S * 2.0 * M * N * K
+    contract_tops = int8_ops / (contract_ms * 1e-3) / 1e12
+
+    out = C.cpu().numpy()
+    want = None
+    if os.path.exists(FIXTURE):
+        with open(FIXTURE) as f:
+            rows = {c["name"]: c for c in json.load(f)["cases"]}
+        if n == 4096:
+            want = rows["c4.adversarial4096"]["out_hash"]
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(A, B, n, out, args.cpu_threads, args.cpu_reps)
+    out_hash = cpu["output_hash"] if cpu else None
+    bit_exact = None
+    if want is not None and out_hash is not None:
+        bit_exact = out_hash == want and cpu["bits_equal_gpu"]
+
+    line = {
+        "metric": "effective FP32 TFLOP/s, S=3 repro GEMM 4096^3; % int8 MFMA peak; bit-exact",
+        "value": round(eff_tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: adversarial dynamic range GEMM, "
+                               "M=N=K=%d, S=3, NN, plan %s %dx%d split %d"
+                               % (n, rg.algo_name(plan.algo), plan.tile_m, plan.tile_n, plan.split_k),
+                   "M": M, "N": N, "K": K, "slices": S},
+        "int8_peak_frac_end_to_end": round(S * S * eff_tflops / PEAK_INT8_TOPS, 4),
+        "stages_ms": {"slice": round(slice_ms, 4), "contract": round(contract_ms, 4),
+                      "final": round(final_ms, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(contract_tops, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "frac": round(contract_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": None,
+                     "kernel": "contract_mfma (int8 ops = 9 * 2MNK per launch, 1 launch/step)"},
+        "cpu_baseline": cpu,
+        "bit_exact": bit_exact,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

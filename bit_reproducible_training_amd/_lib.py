@@ -1,0 +1,100 @@
+"""ctypes bindings of librepro_gemm.so (the C ABI in include/repro_gemm.h).
+
+The library must have been built (bit_reproducible_training_amd._build.build(), or
+__graft_entry__.build()). There is no fallback: if the library is missing or does
+not load, importing this module raises.
+"""
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "librepro_gemm.so")
+
+# hipError_t codes returned by the C ABI.
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+HIP_ERROR_NOT_SUPPORTED = 801
+
+
+class rg_config(ctypes.Structure):
+    _fields_ = [
+        ("split_k", ctypes.c_int),
+        ("tile_m", ctypes.c_int),
+        ("tile_n", ctypes.c_int),
+        ("tile_k", ctypes.c_int),
+        ("algo", ctypes.c_int),
+        ("slices", ctypes.c_int),
+        ("trans_a", ctypes.c_int),
+        ("trans_b", ctypes.c_int),
+    ]
+
+
+class rg_plan(ctypes.Structure):
+    _fields_ = [
+        ("algo", ctypes.c_int),
+        ("split_k", ctypes.c_int),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("tile_m", ctypes.c_int),
+        ("tile_n", ctypes.c_int),
+    ]
+
+
+class rg_layout_info(ctypes.Structure):
+    _fields_ = [
+        ("qa", ctypes.c_size_t),
+        ("qb", ctypes.c_size_t),
+        ("ea", ctypes.c_size_t),
+        ("eb", ctypes.c_size_t),
+        ("part", ctypes.c_longlong),
+        ("Mp", ctypes.c_int),
+        ("Np", ctypes.c_int),
+        ("Kp", ctypes.c_int),
+        ("split_k", ctypes.c_int),
+    ]
+
+
+# Every symbol declared in include/repro_gemm.h, with its ctypes signature.
+_SIGNATURES = {
+    "rg_config_init": (None, [ctypes.POINTER(rg_config)]),
+    "rg_make_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.POINTER(rg_config), ctypes.POINTER(rg_plan)]),
+    "rg_gemm_fp32_ws": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.POINTER(rg_config), ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_void_p, ctypes.c_void_p]),
+    "rg_gemm_fp32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.POINTER(rg_config), ctypes.c_void_p]),
+    "rg_algo_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "rg_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "rg_workspace_layout": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.POINTER(rg_config),
+                                           ctypes.POINTER(rg_layout_info)]),
+    "rg_plan_for_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(rg_plan),
+                                          ctypes.POINTER(rg_layout_info)]),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            "librepro_gemm.so is not built (%s); run __graft_entry__.build() or "
+            "python -m bit_reproducible_training_amd._build" % LIB_PATH)
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def error_string(code):
+    s = lib.rg_error_string(int(code))
+    return s.decode() if s else "hip error %d" % code

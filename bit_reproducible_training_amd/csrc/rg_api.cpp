@@ -1,0 +1,317 @@
+// Host side of librepro_gemm.so: planner, workspace layout, launch sequence and the flat
+// C ABI declared in include/repro_gemm.h.
+//
+// Replaces make_layout / make_plan / launch_quantize / launch_all / repro_gemm_fp32_ws /
+// repro_gemm_fp32 / algo_name (repro_gemm_cuda/repro_gemm.cu:370-542). Stateless apart
+// from a per-device cache of (architecture, compute-unit count); every entry point is
+// re-entrant and stream-ordered.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+
+#include "repro_gemm.h"
+#include "rg_internal.h"
+
+namespace rg {
+namespace {
+
+constexpr size_t ALIGN = 256;
+size_t align_up(size_t x) { return (x + ALIGN - 1) / ALIGN * ALIGN; }
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// Largest |X| the bound check assumes, as the reference defines it
+// (repro_gemm_cuda/repro_gemm.cu:383-388): 127*128^(S-1) + 64*(128^(S-2) + ... + 1).
+double max_fixed_point(int S) {
+    double top = 127.0 * std::ldexp(1.0, 7 * (S - 1)), low = 0.0;
+    for (int t = 0; t < S - 1; ++t) low += 64.0 * std::ldexp(1.0, 7 * t);
+    return top + low;
+}
+
+// Largest |sum over one k of the digit products that share a level|, for balanced
+// base-128 digits (|d0| <= 127, |dp| <= 64 for p > 0):
+//   S=1: 127*127; S=2: level 1 = 2*127*64; S=3: level 2 = 127*64 + 64*64 + 64*127.
+int level_bound_per_k(int S) { return S == 1 ? 16129 : (S == 2 ? 16256 : 20352); }
+
+// Stages (of STEP_K values of k) one part may span with every int32 level sum exact.
+int max_steps_per_part(int S) {
+    long long n = 2147483647LL / level_bound_per_k(S);
+    return (int)(n / STEP_K);
+}
+
+// Row-max pass chunking: enough wavefronts to cover the GPU, at most 16 partials per row.
+void choose_chunks(int R, int K, bool strided, int* nch, int* kch) {
+    int n;
+    if (strided) {
+        int groups = ceil_div(R, 64);
+        n = std::min(ceil_div(2048, groups), std::min(16, ceil_div(K, 64)));
+    } else {
+        n = std::min(ceil_div(2048, R), std::min(16, ceil_div(K, 256)));
+    }
+    n = std::max(1, n);
+    *kch = ceil_div(K, n);
+    *nch = ceil_div(K, *kch);
+}
+
+}  // namespace
+
+int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
+                bool ta, bool tb, const DeviceInfo& dev, Layout* Lp) {
+    if (M <= 0 || N <= 0 || K <= 0 || split_k <= 0) return hipErrorInvalidValue;
+    if (S < 1 || S > 3) return hipErrorInvalidValue;
+    const double d = max_fixed_point(S);
+    if ((double)K * d * d > std::ldexp(1.0, 62)) return hipErrorInvalidValue;
+    if (algo < RG_ALGO_AUTO || algo > RG_ALGO_TENSOR_CORE) return hipErrorInvalidValue;
+
+    Layout L;
+    std::memset(&L, 0, sizeof L);
+    L.S = S;
+    L.M = M;
+    L.N = N;
+    L.K = K;
+    L.ta = ta;
+    L.tb = tb;
+    L.a_strided = ta;   // A stored KxM: row r of op(A) is a column
+    L.b_strided = !tb;  // B stored KxN: column c of op(B) is a column
+    L.Kp = round_up(K, STEP_K);
+
+    if (algo == RG_ALGO_REFERENCE) {
+        L.algo = RG_ALGO_REFERENCE;
+        L.Mp = round_up(M, PANEL_ROWS);
+        L.Np = round_up(N, PANEL_ROWS);
+        L.split = std::min(split_k, K);
+        L.has_partial = true;
+    } else {
+        if (!dev.gfx950) return hipErrorNotSupported;
+        L.algo = algo == RG_ALGO_TILED ? RG_ALGO_TILED : RG_ALGO_TENSOR_CORE;
+        int ti = 0, tj = 0;
+        if (algo == RG_ALGO_TILED) {
+            ti = tj = 1;
+        } else if ((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128)) {
+            ti = tile_m / 64;
+            tj = tile_n / 64;
+        } else {
+            long long big = (long long)ceil_div(M, 128) * ceil_div(N, 128);
+            if (big >= std::max(1, dev.num_cus / 2)) ti = tj = 2;
+            else ti = tj = 1;
+        }
+        L.ti = ti;
+        L.tj = tj;
+        L.Mp = round_up(M, 64 * ti);
+        L.Np = round_up(N, 64 * tj);
+        const int nsteps = L.Kp / STEP_K;
+        const int min_split = ceil_div(nsteps, max_steps_per_part(S));
+        int split = std::max(split_k, min_split);
+        L.split = std::min(split, nsteps);
+        L.has_partial = L.split > 1;
+    }
+
+    choose_chunks(M, K, L.a_strided, &L.nch_a, &L.kch_a);
+    choose_chunks(N, K, L.b_strided, &L.nch_b, &L.kch_b);
+
+    const size_t q_elem = L.algo == RG_ALGO_REFERENCE ? sizeof(int32_t) : (size_t)S;
+    size_t off = 0;
+    L.qa = off;
+    off += align_up((size_t)L.Mp * L.Kp * q_elem);
+    L.qb = off;
+    off += align_up((size_t)L.Np * L.Kp * q_elem);
+    L.ea = off;
+    off += align_up((size_t)L.Mp * sizeof(int));
+    L.eb = off;
+    off += align_up((size_t)L.Np * sizeof(int));
+    L.pma = off;
+    off += align_up((size_t)L.nch_a * L.Mp * sizeof(float));
+    L.pmb = off;
+    off += align_up((size_t)L.nch_b * L.Np * sizeof(float));
+    L.part = off;
+    if (L.has_partial) off += align_up((size_t)L.split * M * N * sizeof(int64_t));
+    L.total = off;
+    *Lp = L;
+    return hipSuccess;
+}
+
+namespace {
+
+struct DevCache {
+    std::atomic<int> state{0};  // 0 unknown, 1 known
+    bool gfx950 = false;
+    int num_cus = 0;
+};
+DevCache g_dev[64];
+
+int query_device(DeviceInfo* info) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 0 && dev < 64 && g_dev[dev].state.load(std::memory_order_acquire) == 1) {
+        info->gfx950 = g_dev[dev].gfx950;
+        info->num_cus = g_dev[dev].num_cus;
+        return hipSuccess;
+    }
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, dev)) != hipSuccess) return e;
+    info->gfx950 = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    info->num_cus = prop.multiProcessorCount;
+    if (dev >= 0 && dev < 64) {
+        g_dev[dev].gfx950 = info->gfx950;
+        g_dev[dev].num_cus = info->num_cus;
+        g_dev[dev].state.store(1, std::memory_order_release);
+    }
+    return hipSuccess;
+}
+
+int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L) {
+    if (!cfg) return hipErrorInvalidValue;
+    DeviceInfo dev{false, 0};
+    if (cfg->algo != RG_ALGO_REFERENCE) {
+        int e = query_device(&dev);
+        if (e != hipSuccess) return e;
+    }
+    return plan_layout(M, N, K, cfg->split_k, cfg->tile_m, cfg->tile_n, cfg->algo, cfg->slices,
+                       cfg->trans_a != 0, cfg->trans_b != 0, dev, L);
+}
+
+}  // namespace
+}  // namespace rg
+
+extern "C" {
+
+void rg_config_init(rg_config* cfg) {
+    if (!cfg) return;
+    cfg->split_k = 1;
+    cfg->tile_m = 16;
+    cfg->tile_n = 16;
+    cfg->tile_k = 32;
+    cfg->algo = RG_ALGO_AUTO;
+    cfg->slices = 3;
+    cfg->trans_a = 0;
+    cfg->trans_b = 0;
+}
+
+int rg_make_plan(int M, int N, int K, const rg_config* cfg, rg_plan* plan) {
+    if (!plan) return hipErrorInvalidValue;
+    rg::Layout L;
+    int e = rg::layout_for_current_device(M, N, K, cfg, &L);
+    if (e != hipSuccess) return e;
+    plan->algo = L.algo;
+    plan->split_k = L.split;
+    plan->workspace_bytes = L.total;
+    plan->tile_m = 64 * L.ti;
+    plan->tile_n = 64 * L.tj;
+    return hipSuccess;
+}
+
+int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
+                       rg_plan* plan, rg_layout_info* info) {
+    if (!cfg || !plan) return hipErrorInvalidValue;
+    rg::DeviceInfo dev{is_gfx950 != 0, num_cus};
+    rg::Layout L;
+    int e = rg::plan_layout(M, N, K, cfg->split_k, cfg->tile_m, cfg->tile_n, cfg->algo,
+                            cfg->slices, cfg->trans_a != 0, cfg->trans_b != 0, dev, &L);
+    if (e != hipSuccess) return e;
+    plan->algo = L.algo;
+    plan->split_k = L.split;
+    plan->workspace_bytes = L.total;
+    plan->tile_m = 64 * L.ti;
+    plan->tile_n = 64 * L.tj;
+    if (info) {
+        info->qa = L.qa;
+        info->qb = L.qb;
+        info->ea = L.ea;
+        info->eb = L.eb;
+        info->part = L.has_partial ? (long long)L.part : -1;
+        info->Mp = L.Mp;
+        info->Np = L.Np;
+        info->Kp = L.Kp;
+        info->split_k = L.split;
+    }
+    return hipSuccess;
+}
+
+int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_info* info) {
+    if (!info) return hipErrorInvalidValue;
+    rg::Layout L;
+    int e = rg::layout_for_current_device(M, N, K, cfg, &L);
+    if (e != hipSuccess) return e;
+    info->qa = L.qa;
+    info->qb = L.qb;
+    info->ea = L.ea;
+    info->eb = L.eb;
+    info->part = L.has_partial ? (long long)L.part : -1;
+    info->Mp = L.Mp;
+    info->Np = L.Np;
+    info->Kp = L.Kp;
+    info->split_k = L.split;
+    return hipSuccess;
+}
+
+int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int K,
+                    const rg_config* cfg, void* workspace, size_t workspace_bytes, void* stream_,
+                    void* const* stage_events) {
+    if (!A || !B || !C) return hipErrorInvalidValue;
+    rg::Layout L;
+    int e = rg::layout_for_current_device(M, N, K, cfg, &L);
+    if (e != hipSuccess) return e;
+    if (!workspace || workspace_bytes < L.total) return hipErrorInvalidValue;
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    auto record = [&](int i) {
+        if (stage_events) (void)hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream);
+    };
+    char* base = static_cast<char*>(workspace);
+    void* qa = base + L.qa;
+    void* qb = base + L.qb;
+    int* ea = reinterpret_cast<int*>(base + L.ea);
+    int* eb = reinterpret_cast<int*>(base + L.eb);
+    float* pma = reinterpret_cast<float*>(base + L.pma);
+    float* pmb = reinterpret_cast<float*>(base + L.pmb);
+    int64_t* part = L.has_partial ? reinterpret_cast<int64_t*>(base + L.part) : nullptr;
+    const bool i32 = L.algo == RG_ALGO_REFERENCE;
+
+    record(0);
+    rg::launch_absmax(A, M, K, L.a_strided, L.nch_a, L.kch_a, L.Mp, pma, stream);
+    rg::launch_absmax(B, N, K, L.b_strided, L.nch_b, L.kch_b, L.Np, pmb, stream);
+    rg::launch_slice(A, M, K, L.Mp, L.Kp, L.a_strided, pma, L.nch_a, L.S, i32, qa, ea, stream);
+    rg::launch_slice(B, N, K, L.Np, L.Kp, L.b_strided, pmb, L.nch_b, L.S, i32, qb, eb, stream);
+    record(1);
+    if (i32)
+        rg::launch_contract_reference(L, static_cast<const int32_t*>(qa),
+                                      static_cast<const int32_t*>(qb), part, stream);
+    else
+        rg::launch_contract_mfma(L, static_cast<const int8_t*>(qa), static_cast<const int8_t*>(qb),
+                                 ea, eb, C, part, stream);
+    record(2);
+    if (L.has_partial) rg::launch_reduce_round(L, part, ea, eb, C, stream);
+    record(3);
+    return hipGetLastError();
+}
+
+int rg_gemm_fp32(const float* A, const float* B, float* C, int M, int N, int K,
+                 const rg_config* cfg, void* stream) {
+    rg_plan plan;
+    int e = rg_make_plan(M, N, K, cfg, &plan);
+    if (e != hipSuccess) return e;
+    void* ws = nullptr;
+    if ((e = hipMalloc(&ws, plan.workspace_bytes)) != hipSuccess) return e;
+    e = rg_gemm_fp32_ws(A, B, C, M, N, K, cfg, ws, plan.workspace_bytes, stream, nullptr);
+    // Synchronise to surface asynchronous kernel errors at this API boundary.
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    (void)hipFree(ws);
+    return e;
+}
+
+const char* rg_algo_name(int algo) {
+    switch (algo) {
+        case RG_ALGO_AUTO: return "auto";
+        case RG_ALGO_REFERENCE: return "ref";
+        case RG_ALGO_TILED: return "tiled";
+        case RG_ALGO_TENSOR_CORE: return "tc";
+        default: return "?";
+    }
+}
+
+const char* rg_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
+
+}  // extern "C"

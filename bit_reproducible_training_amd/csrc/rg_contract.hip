@@ -1,0 +1,222 @@
+// Exact contraction of the sliced operands and the final rounding.
+//
+// Replaces gemm_wmma_i8 / gemm_tiled_dp4a / gemm_reference / reduce_round / write_output
+// (repro_gemm_cuda/repro_gemm.cu:124-165, 189-364).
+//
+// contract_mfma: a 256-thread block (4 wavefronts in 2x2) owns a (64*TI) x (64*TJ) tile of
+// C; each wavefront owns TI x TJ tiles of 32x32 and runs V_MFMA_I32_32X32X32_I8 on them.
+// Digit pairs (p, q) with the same level p + q share one int32 accumulator per output,
+// so a wavefront holds (2S-1) * TI * TJ accumulator tiles. Each pipeline stage copies the
+// block's digit panels for 64 values of k from HBM into LDS (double-buffered); operand
+// fragments are then read from LDS with one 16-byte read per lane and panel. All level
+// accumulators of one output sit in the same lane and register index, so the epilogue
+// combines them in int64 without any data exchange:
+//     T = sum_L acc_L * 2^(7 (2S-2-L)) = sum_k X[r,k] * Y[c,k]   (exact)
+// and either rounds T once to FP32 (one part) or stores it as an int64 partial.
+// Integer addition is associative, so the tile shape, the split and the order of k
+// never change T.
+#include "rg_internal.h"
+#include "repro_gemm_math.h"
+
+namespace rg {
+
+using repro_gemm::round_to_float;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+template <int S, int TI, int TJ>
+__global__ void __launch_bounds__(256, 1)
+contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
+              const int* __restrict__ eA, const int* __restrict__ eB, float* __restrict__ C,
+              int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n) {
+    constexpr int L = 2 * S - 1;
+    constexpr int BM = 64 * TI, BN = 64 * TJ;
+    constexpr int PA = (BM / PANEL_ROWS) * 2 * S;  // A panels per stage
+    constexpr int PB = (BN / PANEL_ROWS) * 2 * S;  // B panels per stage
+    constexpr int PT = PA + PB;
+    constexpr int PW = PT / 4;                     // panels copied per wavefront per stage
+    static_assert(PT % 4 == 0, "stage panels must split evenly over 4 wavefronts");
+    __shared__ v4i lds[2][PT][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+    const int part = blockIdx.y;
+    const int nsteps = Kp / STEP_K;
+    const int s0 = (int)((long long)nsteps * part / split);
+    const int s1 = (int)((long long)nsteps * (part + 1) / split);
+    const size_t row_stride = (size_t)(Kp / PANEL_K) * S * (PANEL_BYTES / 16);  // in v4i
+    const size_t step_stride = (size_t)2 * S * (PANEL_BYTES / 16);              // in v4i
+
+    // Source of each panel this wavefront copies, at step 0.
+    const v4i* src[PW];
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const int pi = wave + 4 * i;
+        if (pi < PA) {
+            const int rl = pi / (2 * S), o = pi % (2 * S);
+            src[i] = reinterpret_cast<const v4i*>(QA) + (size_t)(tm * (BM / PANEL_ROWS) + rl) * row_stride +
+                     (size_t)o * (PANEL_BYTES / 16) + lane;
+        } else {
+            const int pb = pi - PA;
+            const int cl = pb / (2 * S), o = pb % (2 * S);
+            src[i] = reinterpret_cast<const v4i*>(QB) + (size_t)(tn * (BN / PANEL_ROWS) + cl) * row_stride +
+                     (size_t)o * (PANEL_BYTES / 16) + lane;
+        }
+    }
+
+    v16i acc[L][TI][TJ];
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+#pragma unroll
+        for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+            for (int tj = 0; tj < TJ; ++tj)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[l][ti][tj][e] = 0;
+
+    v4i stage[PW];
+    if (s0 < s1) {
+#pragma unroll
+        for (int i = 0; i < PW; ++i) stage[i] = src[i][(size_t)s0 * step_stride];
+#pragma unroll
+        for (int i = 0; i < PW; ++i) lds[0][wave + 4 * i][lane] = stage[i];
+    }
+    __syncthreads();
+
+    for (int s = s0; s < s1; ++s) {
+        const int cur = (s - s0) & 1;
+        const bool more = s + 1 < s1;
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < PW; ++i) stage[i] = src[i][(size_t)(s + 1) * step_stride];
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            v4i a[S][TI], b[S][TJ];
+#pragma unroll
+            for (int p = 0; p < S; ++p) {
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti) a[p][ti] = lds[cur][((wm * TI + ti) * 2 + kk) * S + p][lane];
+#pragma unroll
+                for (int tj = 0; tj < TJ; ++tj) b[p][tj] = lds[cur][PA + ((wn * TJ + tj) * 2 + kk) * S + p][lane];
+            }
+#pragma unroll
+            for (int p = 0; p < S; ++p)
+#pragma unroll
+                for (int q = 0; q < S; ++q)
+#pragma unroll
+                    for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                        for (int tj = 0; tj < TJ; ++tj)
+                            acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                                a[p][ti], b[q][tj], acc[p + q][ti][tj], 0, 0, 0);
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < PW; ++i) lds[cur ^ 1][wave + 4 * i][lane] = stage[i];
+        }
+        __syncthreads();
+    }
+
+    // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
+    // column lane%32.
+    const int e0 = -14 * (S - 1);
+#pragma unroll
+    for (int ti = 0; ti < TI; ++ti) {
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj) {
+            const int rbase = tm * BM + (wm * TI + ti) * 32 + 4 * (lane >> 5);
+            const int col = tn * BN + (wn * TJ + tj) * 32 + (lane & 31);
+            if (col >= N) continue;
+            const int ec = eB[col] + e0;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = rbase + 8 * (e >> 2) + (e & 3);
+                if (row >= M) continue;
+                int64_t t = 0;
+#pragma unroll
+                for (int l = 0; l < L; ++l) t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
+                if (split == 1)
+                    C[(size_t)row * N + col] = round_to_float(t, eA[row] + ec);
+                else
+                    partial[((size_t)part * M + row) * N + col] = t;
+            }
+            // Keep the scheduler from hoisting every accumulator read to the top.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// The definition, as plainly as possible: one thread per output, int64 sum of X * Y over
+// this part's share of k. Always writes an int64 partial.
+__global__ void __launch_bounds__(256)
+contract_reference(const int32_t* __restrict__ X, const int32_t* __restrict__ Y,
+                   int64_t* __restrict__ partial, int M, int N, int K, int Kp, int split) {
+    const int c = blockIdx.x * 16 + (threadIdx.x & 15);
+    const int r = blockIdx.y * 16 + (threadIdx.x >> 4);
+    const int part = blockIdx.z;
+    if (r >= M || c >= N) return;
+    const int k0 = (int)((long long)K * part / split);
+    const int k1 = (int)((long long)K * (part + 1) / split);
+    const int32_t* x = X + (size_t)r * Kp;
+    const int32_t* y = Y + (size_t)c * Kp;
+    int64_t t = 0;
+    for (int k = k0; k < k1; ++k) t += (int64_t)x[k] * y[k];
+    partial[((size_t)part * M + r) * N + c] = t;
+}
+
+// Sums the split partials in int64 (order irrelevant: exact) and rounds once.
+__global__ void __launch_bounds__(256)
+reduce_round(const int64_t* __restrict__ partial, const int* __restrict__ eA,
+             const int* __restrict__ eB, float* __restrict__ C, int M, int N, int split, int e0) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t MN = (size_t)M * N;
+    if (idx >= MN) return;
+    const int r = (int)(idx / N), c = (int)(idx % N);
+    int64_t t = 0;
+    for (int p = 0; p < split; ++p) t += partial[(size_t)p * MN + idx];
+    C[idx] = round_to_float(t, eA[r] + eB[c] + e0);
+}
+
+template <int S>
+static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
+                          const int* eb, float* C, int64_t* partial, hipStream_t stream) {
+    const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
+    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)L.split);
+    if (L.ti == 2 && L.tj == 2)
+        contract_mfma<S, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+    else if (L.ti == 2 && L.tj == 1)
+        contract_mfma<S, 2, 1><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+    else if (L.ti == 1 && L.tj == 2)
+        contract_mfma<S, 1, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+    else
+        contract_mfma<S, 1, 1><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+}
+
+void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
+                          const int* eb, float* C, int64_t* partial, hipStream_t stream) {
+    switch (L.S) {
+        case 1: launch_mfma_s<1>(L, qa, qb, ea, eb, C, partial, stream); break;
+        case 2: launch_mfma_s<2>(L, qa, qb, ea, eb, C, partial, stream); break;
+        case 3: launch_mfma_s<3>(L, qa, qb, ea, eb, C, partial, stream); break;
+        default: break;
+    }
+}
+
+void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,
+                               int64_t* partial, hipStream_t stream) {
+    dim3 grid((unsigned)((L.N + 15) / 16), (unsigned)((L.M + 15) / 16), (unsigned)L.split);
+    contract_reference<<<grid, 256, 0, stream>>>(xa, xb, partial, L.M, L.N, L.K, L.Kp, L.split);
+}
+
+void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,
+                         float* C, hipStream_t stream) {
+    const size_t MN = (size_t)L.M * L.N;
+    unsigned blocks = (unsigned)((MN + 255) / 256);
+    reduce_round<<<blocks, 256, 0, stream>>>(partial, ea, eb, C, L.M, L.N, L.split, -14 * (L.S - 1));
+}
+
+}  // namespace rg

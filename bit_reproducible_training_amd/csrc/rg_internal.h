@@ -1,0 +1,58 @@
+#pragma once
+// Internal declarations shared by the slicing kernels, the contraction kernels and the
+// host API of librepro_gemm.so. Nothing here is part of the public ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace rg {
+
+// Sliced operands are stored in 1 KiB panels of 32 rows x 32 k x one digit, in the
+// order the CDNA4 MFMA reads its operands: byte lane*16 + j of a panel holds element
+// (row = lane % 32, k = 16 * (lane / 32) + j). Panels are laid out
+// [row / 32][k / 32][digit], so one pipeline stage of a block (its row panels x two
+// k panels x S digits) is a few contiguous runs of 2*S KiB.
+constexpr int PANEL_ROWS = 32;
+constexpr int PANEL_K = 32;
+constexpr int PANEL_BYTES = 1024;
+constexpr int STEP_K = 64;  // k consumed per pipeline stage of the contraction
+
+// Where each region lives inside the caller's workspace, and how the work is split.
+struct Layout {
+    int algo;           // resolved RG_ALGO_* (never AUTO)
+    int S, M, N, K;
+    int Mp, Np, Kp;     // padded sizes: Mp, Np multiples of the block tile, Kp of STEP_K
+    int ti, tj;         // MFMA block tile = (64*ti) x (64*tj); 0 for REFERENCE
+    int split;          // split-K parts
+    bool ta, tb;
+    bool a_strided, b_strided;  // operand read along k with a stride (column access)
+    int nch_a, kch_a;   // row-max pass of op(A): chunks along K and chunk length
+    int nch_b, kch_b;
+    bool has_partial;
+    size_t qa, qb, ea, eb, pma, pmb, part, total;  // byte offsets, 256-aligned
+};
+
+// Device facts the planner needs.
+struct DeviceInfo {
+    bool gfx950;
+    int num_cus;
+};
+
+// Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported).
+int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
+                bool ta, bool tb, const DeviceInfo& dev, Layout* L);
+
+// Kernel launchers (asynchronous on `stream`).
+void launch_absmax(const float* src, int R, int K, bool strided, int nch, int kch, int Rp,
+                   float* pmax, hipStream_t stream);
+void launch_slice(const float* src, int R, int K, int Rp, int Kp, bool strided, const float* pmax,
+                  int nch, int S, bool int32_out, void* out, int* expo, hipStream_t stream);
+void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
+                          const int* eb, float* C, int64_t* partial, hipStream_t stream);
+void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,
+                               int64_t* partial, hipStream_t stream);
+void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,
+                         float* C, hipStream_t stream);
+
+}  // namespace rg

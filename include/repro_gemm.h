@@ -1,0 +1,121 @@
+/*
+ * repro_gemm.h -- flat C ABI of the MI355X (gfx950) reproducible FP32 GEMM.
+ *
+ * C[M,N] = op(A)[M,K] * op(B)[K,N], FP32 in and out, row-major, where every row of
+ * op(A) and column of op(B) gets a power-of-two scale, every input is rounded once
+ * to a 7*S-bit integer split into S int8 digits, the digit products are contracted
+ * exactly on CDNA4 int8 MFMA (int32 inside overflow-safe K chunks, int64 across
+ * chunks and split-K), and the exact integer result is rounded once to FP32.
+ * Output bits depend only on the input bits, M, N, K, S and the transposes: never on
+ * tiling, split-K, launch configuration or the GPU.
+ *
+ * Plain C types only (no HIP or torch types): the stream is a hipStream_t passed as
+ * void*, stage events are hipEvent_t passed as void*. Return values are hipError_t
+ * codes: 0 success, 1 invalid value, 801 not supported, others from the HIP runtime.
+ * The C++ interface with the reference's names is repro_gemm.hpp (inline over this).
+ */
+#ifndef REPRO_GEMM_H
+#define REPRO_GEMM_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Algorithm selector; values follow repro_gemm_cuda/repro_gemm.cuh:25-30.
+ * AUTO and TENSOR_CORE run the int8 MFMA contraction with the block tile chosen for
+ * the shape; TILED forces the 64x64 MFMA block tile; REFERENCE is the one-thread-
+ * per-output int64 kernel, kept for verification. */
+enum {
+    RG_ALGO_AUTO = 0,
+    RG_ALGO_REFERENCE = 1,
+    RG_ALGO_TILED = 2,
+    RG_ALGO_TENSOR_CORE = 3
+};
+
+/* repro_gemm_cuda/repro_gemm.cuh:32-41 (same fields, order and defaults).
+ * tile_m/tile_n: the reference ignores them; here a pair naming an MFMA block tile
+ * (128x128, 128x64, 64x128 or 64x64) forces that tile; anything else lets the
+ * planner choose. tile_k is ignored. */
+typedef struct rg_config {
+    int split_k;  /* >= 1; raised automatically when needed for exact int32 sums */
+    int tile_m;   /* default 16 */
+    int tile_n;   /* default 16 */
+    int tile_k;   /* default 32, ignored */
+    int algo;     /* RG_ALGO_*, default RG_ALGO_AUTO */
+    int slices;   /* S in 1..3, default 3 */
+    int trans_a;  /* 0: A is MxK row-major. 1: A is KxM row-major (use A^T) */
+    int trans_b;  /* 0: B is KxN row-major. 1: B is NxK row-major (use B^T) */
+} rg_config;
+
+/* repro_gemm_cuda/repro_gemm.cuh:44-48, plus the block tile actually used. */
+typedef struct rg_plan {
+    int algo;               /* resolved, never RG_ALGO_AUTO */
+    int split_k;            /* effective split count */
+    size_t workspace_bytes; /* size needed by rg_gemm_fp32_ws */
+    int tile_m;             /* block tile rows (MFMA algorithms), 0 for REFERENCE */
+    int tile_n;             /* block tile columns */
+} rg_plan;
+
+/* Fills *cfg with the defaults of repro_gemm::Config. */
+void rg_config_init(rg_config* cfg);
+
+/* Replaces repro_gemm::make_plan (repro_gemm_cuda/repro_gemm.cuh:53, repro_gemm.cu:503-509).
+ * 1 (invalid value): cfg or plan null, M/N/K <= 0, split_k <= 0, slices outside 1..3,
+ *   or K too large for exact int64 at this S (S=3 allows K up to about 1,000,000).
+ * 801 (not supported): an MFMA algorithm on a device that is not gfx950.
+ * Queries the current device for its architecture and compute-unit count. */
+int rg_make_plan(int M, int N, int K, const rg_config* cfg, rg_plan* plan);
+
+/* Replaces repro_gemm::repro_gemm_fp32_ws (repro_gemm_cuda/repro_gemm.cuh:60-66,
+ * repro_gemm.cu:511-528). Asynchronous on `stream` (a hipStream_t; NULL = default
+ * stream), allocates nothing and synchronises nothing. workspace must hold at least
+ * plan.workspace_bytes (hipMalloc alignment); its size depends only on (M, N, K, cfg)
+ * and the device. stage_events, if not NULL, points to 4 hipEvent_t recorded on
+ * `stream` before slicing, after slicing, after the contraction and after the
+ * final rounding. Errors as rg_make_plan, plus 1 for null A/B/C or a workspace that is
+ * null or too small, and any launch error. */
+int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int K,
+                    const rg_config* cfg, void* workspace, size_t workspace_bytes, void* stream,
+                    void* const* stage_events);
+
+/* Replaces repro_gemm::repro_gemm_fp32 (repro_gemm_cuda/repro_gemm.cuh:69-73,
+ * repro_gemm.cu:530-542): allocates the workspace, runs, synchronises the stream to
+ * surface asynchronous errors, frees. */
+int rg_gemm_fp32(const float* A, const float* B, float* C, int M, int N, int K,
+                 const rg_config* cfg, void* stream);
+
+/* Replaces repro_gemm::algo_name (repro_gemm_cuda/repro_gemm.cuh:75, repro_gemm.cu:493-501):
+ * "auto", "ref", "tiled", "tc". */
+const char* rg_algo_name(int algo);
+
+/* Text of a returned error code (hipGetErrorString). */
+const char* rg_error_string(int code);
+
+/* Byte offsets of the internal workspace regions for (M, N, K, cfg) on the current
+ * device, for tests that inspect the sliced operands. No counterpart in the
+ * reference (its layout is private). qa/qb: digit panels of op(A)/op(B); ea/eb:
+ * int32 exponents; part: int64 split-K partials [split][M][N] (or -1 if unused).
+ * Panel layout: [row/32][k/32][digit][1024 bytes], byte (lane*16 + j) of a panel holding
+ * element (row%32 = lane%32, k%32 = 16*(lane/32) + j). Kp (padded K), Mp, Np returned.
+ * REFERENCE stores int32 fixed-point values [Rp][Kp] row-major instead of digits. */
+typedef struct rg_layout_info {
+    size_t qa, qb, ea, eb;
+    long long part;
+    int Mp, Np, Kp;
+    int split_k;
+} rg_layout_info;
+int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_info* info);
+
+/* The planner with an explicit device description instead of a query of the current
+ * device (is_gfx950: 1 if the device is gfx950; num_cus: its compute units), so host
+ * code can plan without a GPU. No counterpart in the reference (its planner always
+ * queries the device, repro_gemm_cuda/repro_gemm.cu:398-408). info may be NULL. */
+int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
+                       rg_plan* plan, rg_layout_info* info);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

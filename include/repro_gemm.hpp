@@ -1,0 +1,96 @@
+#pragma once
+// C++ interface of the reproducible GEMM with the names and signatures of
+// repro_gemm_cuda/repro_gemm.cuh:25-75, on HIP types. Header-only: every function is an
+// inline wrapper over the flat C ABI in repro_gemm.h, so C++ callers (a Conv2d layer,
+// a framework binding, the tests) link only against C symbols of librepro_gemm.so.
+//
+// C[M,N] = op(A)[M,K] * op(B)[K,N], FP32, row-major. The result is bit-identical across
+// runs, split_k values, tile sizes and GPUs, and equal to a CPU implementation of the same
+// definition. S=1: 7-bit inputs, 1 int8 product; S=2: 14-bit, 4; S=3: 21-bit, 9 (default).
+// Inputs must be finite. Do not build with -ffast-math or denormal flushing.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "repro_gemm.h"
+#include "repro_gemm_math.h"
+
+namespace repro_gemm {
+
+enum class Algo {
+    Auto = RG_ALGO_AUTO,             // MFMA contraction, block tile chosen for the shape
+    Reference = RG_ALGO_REFERENCE,   // one thread per output, int64; slow, for verification
+    Tiled = RG_ALGO_TILED,           // MFMA contraction, 64x64 block tile
+    TensorCore = RG_ALGO_TENSOR_CORE // MFMA contraction, block tile chosen for the shape
+};
+
+struct Config {
+    int split_k = 1;        // >= 1. May be raised automatically to keep int32 sums exact.
+    int tile_m = 16;        // a supported MFMA block tile (128/64) forces it; else auto
+    int tile_n = 16;
+    int tile_k = 32;        // ignored
+    Algo algo = Algo::Auto;
+    int slices = 3;         // S, 1..MAX_SLICES
+    bool trans_a = false;   // false: A is MxK row-major.  true: A is KxM row-major (use A^T)
+    bool trans_b = false;   // false: B is KxN row-major.  true: B is NxK row-major (use B^T)
+};
+
+struct Plan {
+    Algo algo;               // resolved (never Auto)
+    int split_k;             // effective split count
+    size_t workspace_bytes;  // size needed by repro_gemm_fp32_ws
+};
+
+inline rg_config to_c(const Config& c) {
+    rg_config r;
+    r.split_k = c.split_k;
+    r.tile_m = c.tile_m;
+    r.tile_n = c.tile_n;
+    r.tile_k = c.tile_k;
+    r.algo = static_cast<int>(c.algo);
+    r.slices = c.slices;
+    r.trans_a = c.trans_a ? 1 : 0;
+    r.trans_b = c.trans_b ? 1 : 0;
+    return r;
+}
+
+// hipErrorNotSupported: cfg.algo cannot run on the current device.
+// hipErrorInvalidValue: bad sizes/slices, or K too large for exact int64 at this S.
+inline hipError_t make_plan(int M, int N, int K, Config cfg, Plan* plan) {
+    if (!plan) return hipErrorInvalidValue;
+    rg_config c = to_c(cfg);
+    rg_plan p;
+    int e = rg_make_plan(M, N, K, &c, &p);
+    if (e == 0) {
+        plan->algo = static_cast<Algo>(p.algo);
+        plan->split_k = p.split_k;
+        plan->workspace_bytes = p.workspace_bytes;
+    }
+    return static_cast<hipError_t>(e);
+}
+
+// Asynchronous, allocation-free version for training loops. workspace must hold at
+// least plan.workspace_bytes. stage_events, if non-null, holds 4 events recorded on
+// `stream` before slicing, after slicing, after the contraction and after the final step.
+inline hipError_t repro_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N,
+                                     int K, Config cfg, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream = nullptr,
+                                     const hipEvent_t* stage_events = nullptr) {
+    rg_config c = to_c(cfg);
+    return static_cast<hipError_t>(rg_gemm_fp32_ws(
+        A, B, C, M, N, K, &c, workspace, workspace_bytes, static_cast<void*>(stream),
+        reinterpret_cast<void* const*>(stage_events)));
+}
+
+// Convenience version: allocates the workspace, runs, synchronizes, frees.
+inline hipError_t repro_gemm_fp32(const float* A, const float* B, float* C, int M, int N, int K,
+                                  Config cfg = Config(), hipStream_t stream = nullptr) {
+    rg_config c = to_c(cfg);
+    return static_cast<hipError_t>(
+        rg_gemm_fp32(A, B, C, M, N, K, &c, static_cast<void*>(stream)));
+}
+
+inline const char* algo_name(Algo a) { return rg_algo_name(static_cast<int>(a)); }
+
+}  // namespace repro_gemm

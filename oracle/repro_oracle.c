@@ -1,0 +1,480 @@
+/*
+ * repro_oracle.c -- CPU restatement of the reproducible FP32 GEMM definition.
+ * TEST INFRASTRUCTURE ONLY (see repro_oracle.h): the product never links this.
+ *
+ * The definition (reference README and repro_gemm_cuda/repro_gemm.cuh:8-21):
+ *   eA[r] = scale_exponent(max_k |op(A)[r,k]|),  eB[c] likewise over op(B)[.,c];
+ *   X[r,k] = fixed_point(op(A)[r,k], eA[r], S),  Y[c,k] = fixed_point(op(B)[k,c], eB[c], S);
+ *   T[r,c] = sum_k X[r,k] * Y[c,k]  exactly (int64);
+ *   C[r,c] = round_to_float(T[r,c], eA[r] + eB[c] - 14 (S - 1)).
+ */
+#include "repro_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------------- */
+/* Scalars                                                                   */
+/* ------------------------------------------------------------------------- */
+
+static uint32_t f2u(float x) { uint32_t b; memcpy(&b, &x, 4); return b; }
+static float u2f(uint32_t b) { float x; memcpy(&x, &b, 4); return x; }
+
+/* x * 2^n as two multiplications by normal powers of two; exact except when the
+ * result is subnormal, where it rounds once (repro_gemm_math.cuh:44-55). */
+float oracle_scale_by_pow2(float x, int n) {
+    int n1 = n >> 1;
+    int n2 = n - n1;
+    float p1 = u2f((uint32_t)(n1 + 127) << 23);
+    float p2 = u2f((uint32_t)(n2 + 127) << 23);
+    float t = x * p1;
+    return t * p2;
+}
+
+/* Smallest e with 2^e >= fl32(m / 127); 0 when m / 127 is zero or m is not positive
+ * (repro_gemm_math.cuh:57-69). For a normal quotient the exponent comes from its bits;
+ * for a subnormal quotient from frexpf. */
+int oracle_scale_exponent(float m) {
+    if (!(m > 0.0f)) return 0;
+    float v = m / 127.0f;
+    uint32_t b = f2u(v);
+    int E = (int)((b >> 23) & 0xFFu);
+    if (E != 0) return (b & 0x7FFFFFu) == 0 ? E - 127 : E - 126;
+    int e;
+    float frac = frexpf(v, &e);
+    if (frac == 0.0f) return 0;
+    return frac == 0.5f ? e - 1 : e;
+}
+
+/* X = RNE(x * 2^(7(S-1) - se)), clamped to |X| <= 127 * 2^(7(S-1))
+ * (repro_gemm_math.cuh:71-83). */
+int oracle_fixed_point(float x, int se, int S) {
+    float v = oracle_scale_by_pow2(x, 7 * (S - 1) - se);
+    int X = (int)nearbyintf(v);
+    int lim = 127 << (7 * (S - 1));
+    return X > lim ? lim : (X < -lim ? -lim : X);
+}
+
+/* Correctly rounded (nearest-even) binary32 value of T * 2^E with subnormals,
+ * signed zero for negative T below the smallest subnormal, and overflow to
+ * infinity (repro_gemm_math.cuh:85-119). */
+float oracle_round_to_float(int64_t T, int E) {
+    if (T == 0) return 0.0f;
+    int neg = T < 0;
+    uint64_t m = neg ? (uint64_t)(-(T + 1)) + 1u : (uint64_t)T;
+    int p = 63 - __builtin_clzll(m);
+    int shift = p - 23;
+    if (-149 - E > shift) shift = -149 - E;
+    uint64_t q;
+    int ex;
+    if (shift <= 0) {
+        q = m;
+        ex = E;
+    } else if (shift >= 64) {
+        q = 0;
+        ex = 0;
+    } else {
+        q = m >> shift;
+        uint64_t rem = m & ((1ull << shift) - 1);
+        uint64_t half = 1ull << (shift - 1);
+        if (rem > half || (rem == half && (q & 1))) ++q;
+        ex = E + shift;
+    }
+    float f = (q != 0 && ex > 127) ? u2f(0x7F800000u) : oracle_scale_by_pow2((float)q, ex);
+    return neg ? -f : f;
+}
+
+void oracle_scale_exponent_n(const float* m, int* e, size_t n) {
+    for (size_t i = 0; i < n; ++i) e[i] = oracle_scale_exponent(m[i]);
+}
+
+void oracle_fixed_point_n(const float* x, const int* se, int S, int* X, size_t n) {
+    for (size_t i = 0; i < n; ++i) X[i] = oracle_fixed_point(x[i], se[i], S);
+}
+
+void oracle_round_to_float_n(const int64_t* T, const int* E, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = oracle_round_to_float(T[i], E[i]);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Thread pool: threads pull indices from one atomic counter                  */
+/* (repro_gemm_cuda/repro_gemm_cpu.h:14-23). Results never depend on it.     */
+/* ------------------------------------------------------------------------- */
+
+typedef void (*body_fn)(void* ctx, int i);
+
+typedef struct {
+    atomic_int next;
+    int n;
+    body_fn fn;
+    void* ctx;
+} pool_t;
+
+static void* pool_worker(void* arg) {
+    pool_t* p = (pool_t*)arg;
+    for (int i; (i = atomic_fetch_add(&p->next, 1)) < p->n;) p->fn(p->ctx, i);
+    return NULL;
+}
+
+static int resolve_threads(int nthreads) {
+    if (nthreads > 0) return nthreads;
+    const char* env = getenv("REPRO_CPU_THREADS");
+    if (env && atoi(env) > 0) return atoi(env);
+    long hc = sysconf(_SC_NPROCESSORS_ONLN);
+    return hc > 0 ? (int)hc : 1;
+}
+
+static void par_for(int n, int nthreads, body_fn fn, void* ctx) {
+    pool_t p;
+    atomic_init(&p.next, 0);
+    p.n = n;
+    p.fn = fn;
+    p.ctx = ctx;
+    if (nthreads <= 1 || n <= 1) {
+        pool_worker(&p);
+        return;
+    }
+    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    int started = 0;
+    for (int t = 0; t < nthreads; ++t)
+        if (pthread_create(&th[t], NULL, pool_worker, &p) == 0) ++started;
+    if (started == 0) pool_worker(&p);
+    for (int t = 0; t < started; ++t) pthread_join(th[t], NULL);
+    free(th);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Independent check of scale_exponent: fl32(m / 127) by exact integer        */
+/* division with round-to-nearest-even, then the smallest power of two >= it. */
+/* ------------------------------------------------------------------------- */
+
+static int scale_exponent_integer(uint32_t bits) {
+    uint32_t be = (bits >> 23) & 0xFFu, fr = bits & 0x7FFFFFu;
+    if (be == 0 && fr == 0) return 0;
+    uint64_t a = be ? (fr | 0x800000u) : fr; /* m = a * 2^q */
+    int q = be ? (int)be - 150 : -149;
+    uint64_t num = a << 40;                  /* m / 127 = (N + rem/127) * 2^(q-40) */
+    uint64_t N = num / 127u, rem = num % 127u;
+    int p = 63 - __builtin_clzll(N);
+    int d = p - 23;                          /* bits to drop for 24 significant bits */
+    if (-149 - (q - 40) > d) d = -149 - (q - 40); /* nothing below 2^-149 */
+    uint64_t kept = N >> d, low = N & ((1ull << d) - 1), half = 1ull << (d - 1);
+    if (low > half || (low == half && (rem != 0 || (kept & 1)))) ++kept;
+    if (kept == 0) return 0;                 /* the quotient rounded to zero */
+    int w = q - 40 + d;                      /* v = kept * 2^w */
+    int pk = 63 - __builtin_clzll(kept);
+    return (kept == (1ull << pk)) ? pk + w : pk + w + 1;
+}
+
+typedef struct {
+    uint32_t lo, hi;
+    int chunks;
+    atomic_ullong bad;
+    atomic_uint first;
+} se_check_t;
+
+static void se_check_body(void* ctx, int i) {
+    se_check_t* c = (se_check_t*)ctx;
+    uint64_t span = (uint64_t)c->hi - c->lo;
+    uint32_t a = c->lo + (uint32_t)(span * (uint64_t)i / (uint64_t)c->chunks);
+    uint32_t b = c->lo + (uint32_t)(span * (uint64_t)(i + 1) / (uint64_t)c->chunks);
+    uint64_t bad = 0;
+    uint32_t first = 0xFFFFFFFFu;
+    for (uint32_t x = a; x < b; ++x) {
+        if (oracle_scale_exponent(u2f(x)) != scale_exponent_integer(x)) {
+            if (!bad) first = x;
+            ++bad;
+        }
+    }
+    if (bad) {
+        atomic_fetch_add(&c->bad, bad);
+        uint32_t cur = atomic_load(&c->first);
+        while (first < cur && !atomic_compare_exchange_weak(&c->first, &cur, first)) {
+        }
+    }
+}
+
+uint64_t oracle_check_scale_exponent_range(uint32_t lo, uint32_t hi, uint32_t* first) {
+    se_check_t c;
+    c.lo = lo;
+    c.hi = hi;
+    c.chunks = 1024;
+    atomic_init(&c.bad, 0);
+    atomic_init(&c.first, 0xFFFFFFFFu);
+    if (hi > lo) par_for(c.chunks, resolve_threads(0), se_check_body, &c);
+    if (first) *first = atomic_load(&c.first);
+    return atomic_load(&c.bad);
+}
+
+/* ------------------------------------------------------------------------- */
+/* The GEMM                                                                  */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K, ta, tb, S, r0;
+    int32_t* X;
+    int32_t* Y;
+    int* eA;
+    int* eB;
+    int64_t* T;
+} gemm_ctx;
+
+static float a_at(const gemm_ctx* g, int r, int k) {
+    return g->ta ? g->A[(size_t)k * g->M + r] : g->A[(size_t)r * g->K + k];
+}
+static float b_at(const gemm_ctx* g, int k, int c) {
+    return g->tb ? g->B[(size_t)c * g->K + k] : g->B[(size_t)k * g->N + c];
+}
+
+/* repro_gemm_cpu.h:30-35: row max, exponent, fixed point of every element of row r. */
+static void quant_row(void* ctx, int r) {
+    gemm_ctx* g = (gemm_ctx*)ctx;
+    float m = 0.0f;
+    for (int k = 0; k < g->K; ++k) m = fmaxf(m, fabsf(a_at(g, r, k)));
+    int e = oracle_scale_exponent(m);
+    g->eA[r] = e;
+    int32_t* x = g->X + (size_t)r * g->K;
+    for (int k = 0; k < g->K; ++k) x[k] = oracle_fixed_point(a_at(g, r, k), e, g->S);
+}
+
+/* repro_gemm_cpu.h:36-41: the same per column of op(B), stored transposed. */
+static void quant_col(void* ctx, int c) {
+    gemm_ctx* g = (gemm_ctx*)ctx;
+    float m = 0.0f;
+    for (int k = 0; k < g->K; ++k) m = fmaxf(m, fabsf(b_at(g, k, c)));
+    int e = oracle_scale_exponent(m);
+    g->eB[c] = e;
+    int32_t* y = g->Y + (size_t)c * g->K;
+    for (int k = 0; k < g->K; ++k) y[k] = oracle_fixed_point(b_at(g, k, c), e, g->S);
+}
+
+/* repro_gemm_cpu.h:42-50: exact int64 dot products, one rounding per output. */
+static void dot_row(void* ctx, int i) {
+    gemm_ctx* g = (gemm_ctx*)ctx;
+    int r = g->r0 + i;
+    const int32_t* x = g->X + (size_t)r * g->K;
+    for (int c = 0; c < g->N; ++c) {
+        const int32_t* y = g->Y + (size_t)c * g->K;
+        int64_t t = 0;
+        for (int k = 0; k < g->K; ++k) t += (int64_t)x[k] * y[k];
+        g->C[(size_t)i * g->N + c] = oracle_round_to_float(t, g->eA[r] + g->eB[c] - 14 * (g->S - 1));
+    }
+}
+
+static void exact_row(void* ctx, int r) {
+    gemm_ctx* g = (gemm_ctx*)ctx;
+    const int32_t* x = g->X + (size_t)r * g->K;
+    for (int c = 0; c < g->N; ++c) {
+        const int32_t* y = g->Y + (size_t)c * g->K;
+        int64_t t = 0;
+        for (int k = 0; k < g->K; ++k) t += (int64_t)x[k] * y[k];
+        g->T[(size_t)r * g->N + c] = t;
+    }
+}
+
+void oracle_quantize(const float* A, const float* B, int M, int N, int K, int ta, int tb, int S,
+                     int32_t* X, int32_t* Y, int* eA, int* eB, int nthreads) {
+    gemm_ctx g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.B = B; g.M = M; g.N = N; g.K = K; g.ta = ta; g.tb = tb; g.S = S;
+    g.X = X; g.Y = Y; g.eA = eA; g.eB = eB;
+    int nt = resolve_threads(nthreads);
+    par_for(M, nt, quant_row, &g);
+    par_for(N, nt, quant_col, &g);
+}
+
+void oracle_exact_products(const int32_t* X, const int32_t* Y, int64_t* T, int M, int N, int K,
+                           int nthreads) {
+    gemm_ctx g;
+    memset(&g, 0, sizeof g);
+    g.M = M; g.N = N; g.K = K;
+    g.X = (int32_t*)X; g.Y = (int32_t*)Y; g.T = T;
+    par_for(M, resolve_threads(nthreads), exact_row, &g);
+}
+
+static void quant_row_off(void* ctx, int i) { quant_row(ctx, ((gemm_ctx*)ctx)->r0 + i); }
+
+int oracle_cpu_gemm_rows(const float* A, const float* B, float* C, int M, int N, int K, int ta,
+                         int tb, int S, int r0, int r1, int nthreads) {
+    int nt = resolve_threads(nthreads);
+    if (M <= 0 || N <= 0 || K <= 0 || r0 < 0 || r1 > M || r0 >= r1) return nt;
+    gemm_ctx g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.B = B; g.C = C; g.M = M; g.N = N; g.K = K; g.ta = ta; g.tb = tb; g.S = S;
+    g.r0 = r0;
+    g.X = (int32_t*)malloc(sizeof(int32_t) * (size_t)M * (size_t)K);
+    g.Y = (int32_t*)malloc(sizeof(int32_t) * (size_t)N * (size_t)K);
+    g.eA = (int*)malloc(sizeof(int) * (size_t)M);
+    g.eB = (int*)malloc(sizeof(int) * (size_t)N);
+    if (g.X && g.Y && g.eA && g.eB) {
+        par_for(r1 - r0, nt, quant_row_off, &g); /* only the rows that are computed */
+        par_for(N, nt, quant_col, &g);
+        par_for(r1 - r0, nt, dot_row, &g);
+    }
+    free(g.X); free(g.Y); free(g.eA); free(g.eB);
+    return nt;
+}
+
+int oracle_cpu_gemm(const float* A, const float* B, float* C, int M, int N, int K, int ta, int tb,
+                    int S, int nthreads) {
+    return oracle_cpu_gemm_rows(A, B, C, M, N, K, ta, tb, S, 0, M, nthreads);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Portable inputs and hashing                                               */
+/* ------------------------------------------------------------------------- */
+
+/* SplitMix64 (repro_test_util.h:30-37): the generator adds the golden gamma to its state
+ * and mixes; draw i of the stream seeded with s is therefore mix(s + (i+1) * gamma), which
+ * lets the generators below fill disjoint ranges in parallel with identical bits. */
+static uint64_t sm_mix(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+static uint64_t sm_draw(uint64_t seed, uint64_t i) { return sm_mix(seed + (i + 1) * 0x9e3779b97f4a7c15ull); }
+
+/* 24 random bits scaled to [0, 1): exact in double (repro_test_util.h:38). */
+static double sm_u01_at(uint64_t seed, uint64_t i) { return (double)(sm_draw(seed, i) >> 40) * (1.0 / 16777216.0); }
+
+void oracle_splitmix64(uint64_t* out, size_t n, uint64_t seed) {
+    for (size_t i = 0; i < n; ++i) out[i] = sm_draw(seed, i);
+}
+
+enum { GEN_NORMAL, GEN_UNIFORM, GEN_UNIFORM_PM, GEN_ADVERSARIAL };
+
+typedef struct {
+    float* out;
+    size_t n;
+    double scale;
+    uint64_t seed, first;
+    int kind;
+    int chunks;
+    int cols;      /* adversarial: row length */
+    int pair_rows; /* adversarial: pairs are (r, r^1) instead of (c, c^1) */
+    int negate;    /* adversarial: second of a pair is negated */
+} gen_ctx;
+
+/* Adversarial base element: 5% exact zeros, 1% subnormals, otherwise +-2^e with e uniform
+ * in [-60, 60]. */
+static float adversarial_base(uint64_t seed, uint64_t idx) {
+    uint64_t u = sm_draw(seed, 2 * idx);
+    uint64_t v = sm_draw(seed, 2 * idx + 1);
+    unsigned pct = (unsigned)(u % 100u);
+    uint32_t sign = (uint32_t)((v >> 63) & 1u) << 31;
+    uint32_t bits;
+    if (pct < 5) {
+        bits = 0;
+    } else if (pct < 6) {
+        uint32_t f = (uint32_t)((v >> 8) & 0x7FFFFFu);
+        bits = f ? f : 1u;
+    } else {
+        int e = (int)((v >> 16) % 121u) - 60;
+        bits = (uint32_t)(e + 127) << 23;
+    }
+    uint32_t b = sign | bits;
+    float x;
+    memcpy(&x, &b, 4);
+    return x;
+}
+
+static void gen_body(void* vctx, int c) {
+    gen_ctx* g = (gen_ctx*)vctx;
+    size_t a = g->n * (size_t)c / (size_t)g->chunks, b = g->n * (size_t)(c + 1) / (size_t)g->chunks;
+    for (size_t i = a; i < b; ++i) {
+        uint64_t idx = g->first + i;
+        switch (g->kind) {
+            case GEN_NORMAL: {
+                double t = 0.0;
+                for (int j = 0; j < 12; ++j) t += sm_u01_at(g->seed, 12 * idx + (uint64_t)j);
+                g->out[i] = (float)(g->scale * (t - 6.0));
+                break;
+            }
+            case GEN_UNIFORM:
+                g->out[i] = (float)(g->scale * sm_u01_at(g->seed, idx));
+                break;
+            case GEN_UNIFORM_PM: {
+                /* float32 arithmetic as repro_torch/utils.py:23-29: u = bits * 2^-24 (exact),
+                 * v = u * (2 * bound) - bound, each a single float32 rounding. */
+                float bound = (float)g->scale;
+                float u = (float)(sm_draw(g->seed, idx) >> 40) * (1.0f / 16777216.0f);
+                float two_b = 2.0f * bound;
+                float t = u * two_b;
+                g->out[i] = t - bound;
+                break;
+            }
+            case GEN_ADVERSARIAL: {
+                /* Elements come in pairs along k: the second of a pair is the first times
+                 * (1 + 2^-20 t), t in {-1, 0, 1}, and negated when g->negate is set. An
+                 * operand with negated pairs times one with plain pairs cancels almost
+                 * exactly in every dot product. */
+                size_t r = i / (size_t)g->cols, c = i % (size_t)g->cols;
+                size_t base, second;
+                if (g->pair_rows) {
+                    base = (r & ~(size_t)1) * (size_t)g->cols + c;
+                    second = r & 1;
+                } else {
+                    base = r * (size_t)g->cols + (c & ~(size_t)1);
+                    second = c & 1;
+                }
+                float x = adversarial_base(g->seed, base);
+                if (second) {
+                    uint64_t w = sm_draw(g->seed ^ 0x5bd1e995ull, base);
+                    int t = (int)(w % 3u) - 1;
+                    float f = 1.0f + (float)t * (1.0f / 1048576.0f);
+                    x = x * f;
+                    if (g->negate) x = -x;
+                }
+                g->out[i] = x;
+                break;
+            }
+        }
+    }
+}
+
+static void gen_run(float* out, size_t n, double scale, uint64_t seed, uint64_t first, int kind, int cols) {
+    gen_ctx g;
+    memset(&g, 0, sizeof g);
+    g.out = out; g.n = n; g.scale = scale; g.seed = seed; g.first = first; g.kind = kind;
+    g.cols = cols > 0 ? cols : 1;
+    g.chunks = n < 65536 ? 1 : 256;
+    par_for(g.chunks, g.chunks == 1 ? 1 : resolve_threads(0), gen_body, &g);
+}
+
+/* Irwin-Hall: sum of twelve U[0,1) minus 6, exact in double (repro_test_util.h:41). */
+void oracle_gen_normal(float* out, size_t n, double scale, uint64_t seed) {
+    gen_run(out, n, scale, seed, 0, GEN_NORMAL, 0);
+}
+void oracle_gen_normal_at(float* out, size_t n, double scale, uint64_t seed, uint64_t first_elem) {
+    gen_run(out, n, scale, seed, first_elem, GEN_NORMAL, 0);
+}
+void oracle_gen_uniform(float* out, size_t n, double scale, uint64_t seed) {
+    gen_run(out, n, scale, seed, 0, GEN_UNIFORM, 0);
+}
+void oracle_gen_uniform_pm(float* out, size_t n, float bound, uint64_t seed, uint64_t first_elem) {
+    gen_run(out, n, (double)bound, seed, first_elem, GEN_UNIFORM_PM, 0);
+}
+void oracle_gen_adversarial(float* out, int rows, int cols, uint64_t seed, int pair_rows, int negate) {
+    gen_ctx g;
+    memset(&g, 0, sizeof g);
+    g.out = out; g.n = (size_t)rows * (size_t)cols; g.scale = 1.0; g.seed = seed;
+    g.kind = GEN_ADVERSARIAL; g.cols = cols; g.pair_rows = pair_rows; g.negate = negate;
+    g.chunks = g.n < 65536 ? 1 : 256;
+    par_for(g.chunks, g.chunks == 1 ? 1 : resolve_threads(0), gen_body, &g);
+}
+
+uint64_t oracle_fnv1a64(const void* data, size_t n, uint64_t h) {
+    const unsigned char* p = (const unsigned char*)data;
+    for (size_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}

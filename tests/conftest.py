@@ -1,0 +1,38 @@
+import os
+import sys
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+for p in (REPO, HERE):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    config.addinivalue_line("markers", "slow: takes more than a few seconds")
+
+
+def _ensure_built():
+    """Builds the HIP library and the oracle only if they are missing."""
+    lib = os.path.join(REPO, "bit_reproducible_training_amd", "librepro_gemm.so")
+    if not os.path.exists(lib):
+        from bit_reproducible_training_amd import _build
+
+        _build.build()
+    if not os.path.exists(os.path.join(REPO, "oracle", "liboracle.so")):
+        from oracle import oracle  # noqa: F401  (builds on import when missing)
+
+
+_ensure_built()
+
+
+@pytest.fixture(scope="session")
+def torch_gpu():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test requested but torch.cuda is not available")
+    return torch

@@ -1,0 +1,54 @@
+"""Writes tests/golden/baseline_configs.json: input and output FNV-1a-64 hashes of every
+BASELINE configuration case (recipes in configs.py), computed with the CPU oracle
+(oracle/repro_oracle.c, itself pinned to the reference's recorded suite hashes) and,
+where it is built and the case is small enough, cross-checked against the reference's
+own CPU path (oracle/_ref).
+
+Run from the repository root:  python tests/golden/make_golden.py
+"""
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, REPO)
+sys.path.insert(0, os.path.dirname(HERE))
+
+from golden import configs  # noqa: E402
+from oracle import oracle as O  # noqa: E402
+
+OUT = os.path.join(HERE, "baseline_configs.json")
+REF_CHECK_MAX_MACS = 2e10
+
+
+def main():
+    rows = []
+    for case in configs.all_cases():
+        t0 = time.time()
+        A, B = case["make"]()
+        M, N, K = case["M"], case["N"], case["K"]
+        hin = O.fnv_chain(A, B)
+        C = O.cpu_gemm(A, B, M, N, K, case["ta"], case["tb"], case["S"])
+        hout = O.fnv1a64(C)
+        ref_checked = False
+        if O.ref is not None and float(M) * N * K <= REF_CHECK_MAX_MACS:
+            R = O.ref_cpu_gemm(A, B, M, N, K, case["ta"], case["tb"], case["S"])
+            if O.fnv1a64(R) != hout:
+                raise SystemExit("oracle and reference CPU path disagree on " + case["name"])
+            ref_checked = True
+        nonfinite = int((~__import__("numpy").isfinite(C)).sum())
+        rows.append(dict(name=case["name"], M=M, N=N, K=K, ta=case["ta"], tb=case["tb"],
+                         S=case["S"], in_hash="%016x" % hin, out_hash="%016x" % hout,
+                         ref_checked=ref_checked, nonfinite=nonfinite))
+        print("%-28s %016x %016x ref=%d %.1fs" % (case["name"], hin, hout, ref_checked,
+                                                 time.time() - t0), flush=True)
+        del A, B, C
+    with open(OUT, "w") as f:
+        json.dump({"generator": "tests/golden/make_golden.py", "cases": rows}, f, indent=1)
+    print("wrote", OUT)
+
+
+if __name__ == "__main__":
+    main()

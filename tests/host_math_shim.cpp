@@ -1,0 +1,32 @@
+// Host build of the product's scalar header (include/repro_gemm_math.h), so CPU tests can
+// compare its integer formulations with the oracle on every input they choose. The GPU
+// tests then compare the device build of the same header with this host build.
+#include <cstdint>
+
+#include "repro_gemm_math.h"
+
+extern "C" {
+
+void hm_scale_exponent_n(const float* m, int* e, long long n) {
+    for (long long i = 0; i < n; ++i) e[i] = repro_gemm::scale_exponent(m[i]);
+}
+
+// Every float with bit pattern in [lo, hi): number whose exponent differs from `want_fn`'s.
+long long hm_scale_exponent_count_range(uint32_t lo, uint32_t hi, int (*want_fn)(float)) {
+    long long bad = 0;
+    for (uint32_t b = lo; b < hi; ++b) {
+        float x = repro_gemm::bits_to_float(b);
+        if (repro_gemm::scale_exponent(x) != want_fn(x)) ++bad;
+    }
+    return bad;
+}
+
+void hm_fixed_point_n(const float* x, const int* se, int S, int* out, long long n) {
+    for (long long i = 0; i < n; ++i) out[i] = repro_gemm::fixed_point(x[i], se[i], S);
+}
+
+void hm_round_to_float_n(const int64_t* T, const int* E, float* out, long long n) {
+    for (long long i = 0; i < n; ++i) out[i] = repro_gemm::round_to_float(T[i], E[i]);
+}
+
+}  // extern "C"

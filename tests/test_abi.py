@@ -1,0 +1,158 @@
+"""The C ABI library on the host: it loads, exports every symbol include/repro_gemm.h
+declares, and its planner behaves as the reference's make_plan does
+(repro_gemm_cuda/repro_gemm.cu:390-439, 503-509). No kernel is launched here."""
+import ctypes
+import math
+import os
+import re
+
+import pytest
+
+import bit_reproducible_training_amd as rg
+from bit_reproducible_training_amd import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    with open(os.path.join(REPO, "include", "repro_gemm.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(rg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    declared = _declared_symbols()
+    assert declared, "no declarations found"
+    for name in declared:
+        assert hasattr(_lib.lib, name), name
+    assert set(declared) == set(_lib.EXPORTED)
+
+
+def test_config_defaults_match_reference():
+    c = _lib.rg_config()
+    _lib.lib.rg_config_init(ctypes.byref(c))
+    assert (c.split_k, c.tile_m, c.tile_n, c.tile_k, c.algo, c.slices, c.trans_a, c.trans_b) == \
+        (1, 16, 16, 32, 0, 3, 0, 0)
+    d = rg.Config()
+    assert (d.split_k, d.tile_m, d.tile_n, d.tile_k, int(d.algo), d.slices) == (1, 16, 16, 32, 0, 3)
+
+
+def test_algo_names():
+    assert [rg.algo_name(a) for a in (0, 1, 2, 3)] == ["auto", "ref", "tiled", "tc"]
+    assert rg.algo_name(9) == "?"
+
+
+def _plan(M, N, K, **kw):
+    return rg.plan_for_device(M, N, K, rg.Config(**kw), is_gfx950=True, num_cus=256)
+
+
+@pytest.mark.parametrize("args", [(0, 4, 4), (4, 0, 4), (4, 4, 0), (-1, 4, 4)])
+def test_invalid_sizes(args):
+    with pytest.raises(rg.ReproGemmError) as e:
+        _plan(*args)
+    assert e.value.code == _lib.HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("kw", [dict(split_k=0), dict(slices=0), dict(slices=4), dict(algo=7)])
+def test_invalid_config(kw):
+    with pytest.raises(rg.ReproGemmError) as e:
+        _plan(64, 64, 64, **kw)
+    assert e.value.code == _lib.HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("S", [1, 2, 3])
+def test_k_bound_for_exact_int64(S):
+    # K * maxX^2 <= 2^62 with maxX = 127*128^(S-1) + 64*sum_{t<S-1} 128^t
+    d = 127 * 128 ** (S - 1) + sum(64 * 128 ** t for t in range(S - 1))
+    kmax = (2 ** 62) // (d * d)
+    kmax = min(kmax, 2 ** 31 - 1)
+    if kmax < 2 ** 31 - 1:
+        _plan(1, 1, kmax, slices=S)
+        with pytest.raises(rg.ReproGemmError):
+            _plan(1, 1, kmax + 1, slices=S)
+    if S == 3:
+        assert 1_000_000 < kmax < 1_100_000  # "S=3 allows K up to about 1,000,000"
+
+
+def test_not_supported_off_gfx950():
+    with pytest.raises(rg.ReproGemmError) as e:
+        rg.plan_for_device(64, 64, 64, rg.Config(), is_gfx950=False, num_cus=256)
+    assert e.value.code == _lib.HIP_ERROR_NOT_SUPPORTED
+    p, _ = rg.plan_for_device(64, 64, 64, rg.Config(algo=rg.Algo.Reference), is_gfx950=False,
+                              num_cus=256)
+    assert p.algo == rg.Algo.Reference
+
+
+def test_auto_resolves_to_mfma():
+    p, _ = _plan(4096, 4096, 4096)
+    assert p.algo == rg.Algo.TensorCore and (p.tile_m, p.tile_n) == (128, 128)
+    p, _ = _plan(64, 10, 84)
+    assert p.algo == rg.Algo.TensorCore and (p.tile_m, p.tile_n) == (64, 64)
+    p, _ = _plan(256, 256, 256, algo=rg.Algo.Tiled)
+    assert p.algo == rg.Algo.Tiled and (p.tile_m, p.tile_n) == (64, 64)
+
+
+@pytest.mark.parametrize("tm,tn", [(128, 128), (128, 64), (64, 128), (64, 64)])
+def test_tile_hints(tm, tn):
+    p, info = _plan(300, 200, 100, tile_m=tm, tile_n=tn)
+    assert (p.tile_m, p.tile_n) == (tm, tn)
+    assert info.Mp % tm == 0 and info.Np % tn == 0 and info.Mp >= 300 and info.Np >= 200
+
+
+@pytest.mark.parametrize("S,limit", [(1, 133120), (2, 132096), (3, 105472)])
+def test_split_raised_for_exact_int32(S, limit):
+    """Each part spans at most floor((2^31-1) / level_bound / 64) * 64 values of k."""
+    p, _ = _plan(64, 64, limit, slices=S)
+    assert p.split_k == 1
+    p, _ = _plan(64, 64, limit + 64, slices=S)
+    assert p.split_k == 2
+    p, _ = _plan(64, 64, 3 * limit, slices=S, split_k=1)
+    assert p.split_k == 3
+
+
+def test_split_clamped_to_k_steps():
+    p, _ = _plan(64, 64, 100, split_k=64)
+    assert p.split_k == 2  # Kp = 128 -> two stages of 64
+    p, _ = _plan(64, 64, 7, split_k=64, algo=rg.Algo.Reference)
+    assert p.split_k == 7  # the reference path clamps split to K
+
+
+def test_workspace_layout_regions():
+    for kw in (dict(), dict(split_k=4), dict(algo=rg.Algo.Reference, split_k=3), dict(slices=1)):
+        p, info = _plan(133, 77, 301, **kw)
+        S = kw.get("slices", 3)
+        elem = 4 if kw.get("algo") == rg.Algo.Reference else S
+        assert info.qa % 256 == 0 and info.qb % 256 == 0 and info.ea % 256 == 0
+        assert info.qb >= info.qa + info.Mp * info.Kp * elem
+        assert info.ea >= info.qb + info.Np * info.Kp * elem
+        assert info.Kp % 64 == 0 and info.Kp >= 301
+        if p.split_k > 1:
+            assert info.part >= 0
+            assert p.workspace_bytes >= info.part + p.split_k * 133 * 77 * 8
+        else:
+            assert info.part == -1
+        assert p.workspace_bytes % 256 == 0
+
+
+def test_workspace_depends_only_on_shape_and_config():
+    a, _ = _plan(1000, 1000, 1000)
+    b, _ = _plan(1000, 1000, 1000)
+    assert a == b
+
+
+def test_reference_plan_needs_no_device():
+    """The Reference algorithm never queries the device (like the reference, which queries
+    only for Auto/TensorCore): make_plan works on a host without a GPU."""
+    p = rg.make_plan(133, 77, 301, rg.Config(algo=rg.Algo.Reference))
+    assert p.algo == rg.Algo.Reference and p.split_k == 1
+
+
+def test_null_pointers_rejected_before_any_launch():
+    c = rg.Config(algo=rg.Algo.Reference)
+    assert rg.repro_gemm_fp32_ws(None, 1, 1, 4, 4, 4, c, 1, 1 << 20) == _lib.HIP_ERROR_INVALID_VALUE
+    assert rg.repro_gemm_fp32_ws(1, 1, 1, 4, 4, 4, c, None, 1 << 20) == _lib.HIP_ERROR_INVALID_VALUE
+    assert rg.repro_gemm_fp32_ws(1, 1, 1, 4, 4, 4, c, 1, 1) == _lib.HIP_ERROR_INVALID_VALUE
+
+
+def test_max_fixed_point_constant():
+    assert math.isclose(127 * 128 ** 2 + 64 * 129, 2089024)

@@ -1,0 +1,243 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle, bit for bit.
+
+Mirrors the reference's correctness suite (repro_gemm_cuda/test_repro_gemm.cu:17-81),
+hash tool checks (hash_repro_gemm.cu:79-204) and recorded suite hashes
+(gpt2_ops_suite/results/mac/cpu.txt), plus stage-level checks of the slicing kernel
+(digits and exponents) and of the contraction (exact int64 products).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import bit_reproducible_training_amd as rg
+from gpu_util import bits, decode_digits, note, run, to_dev
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+ALGOS = [rg.Algo.Reference, rg.Algo.Tiled, rg.Algo.TensorCore, rg.Algo.Auto]
+
+
+def _transposed(A, B, M, N, K, ta, tb):
+    At = np.ascontiguousarray(A.reshape(M, K).T) if ta else A
+    Bt = np.ascontiguousarray(B.reshape(K, N).T) if tb else B
+    return At, Bt
+
+
+def test_config1_all_algorithms(torch_gpu):
+    torch = torch_gpu
+    with open(os.path.join(GOLDEN, "baseline_configs.json")) as f:
+        fx = {c["name"]: c for c in json.load(f)["cases"]}
+    n = 256 * 256
+    A = O.gen_normal(n, 1.0, 12345, 0)
+    B = O.gen_normal(n, 1.0, 12345, n)
+    want = O.cpu_gemm(A, B, 256, 256, 256, 0, 0, 3)
+    assert "%016x" % O.fnv1a64(want) == fx["c1.256cube"]["out_hash"]
+    for algo in ALGOS:
+        note("config1 algo", algo.name)
+        C, plan, _ = run(torch, A, B, 256, 256, 256, rg.Config(algo=algo))
+        assert np.array_equal(bits(C), want.view(np.uint32)), algo.name
+
+
+@pytest.mark.parametrize("S", [1, 2, 3])
+def test_reference_correctness_suite(torch_gpu, S):
+    """test_repro_gemm.cu restated: 133x77x301 (not tile multiples), N(0,1) with one 1e6
+    outlier; every algorithm x split_k {1,2,3,7,64} x transposes, plus a repeat run,
+    each compared bit for bit with the CPU definition, output poisoned before each run."""
+    torch = torch_gpu
+    M, N, K = 133, 77, 301
+    A = O.gen_normal(M * K, 1.0, 2024, 0)
+    B = O.gen_normal(K * N, 1.0, 2024, M * K)
+    A[5] = 1e6
+    want = O.cpu_gemm(A, B, M, N, K, 0, 0, S).view(np.uint32)
+    At, _ = _transposed(A, B, M, N, K, 1, 0)
+    _, Bt = _transposed(A, B, M, N, K, 0, 1)
+    dA, dB, dAt, dBt = (to_dev(torch, x) for x in (A, B, At, Bt))
+    ws = None
+    for algo in ALGOS[:3]:
+        for split in (1, 2, 3, 7, 64):
+            for ta, tb in ((0, 0), (0, 0), (1, 0), (1, 1), (0, 1)):
+                note("suite S=%d algo=%s split=%d ta=%d tb=%d" % (S, algo.name, split, ta, tb))
+                cfg = rg.Config(algo=algo, slices=S, split_k=split, trans_a=ta, trans_b=tb)
+                C, _, ws = run(torch, dAt if ta else dA, dBt if tb else dB, M, N, K, cfg, ws=ws)
+                assert np.array_equal(bits(C), want), (algo.name, split, ta, tb)
+
+
+def test_tile_and_split_invariance(torch_gpu):
+    torch = torch_gpu
+    M, N, K = 600, 520, 2100
+    A = O.gen_normal(M * K, 1.0, 31)
+    B = O.gen_normal(N * K, 0.02, 32)
+    want = O.cpu_gemm(A, B, M, N, K, 0, 1, 3).view(np.uint32)
+    dA, dB = to_dev(torch, A), to_dev(torch, B)
+    ws = None
+    for tm, tn in ((128, 128), (128, 64), (64, 128), (64, 64)):
+        for split in (1, 2, 5, 16, 33):
+            note("tiles %dx%d split %d" % (tm, tn, split))
+            cfg = rg.Config(tile_m=tm, tile_n=tn, split_k=split, trans_b=True)
+            C, plan, ws = run(torch, dA, dB, M, N, K, cfg, ws=ws)
+            assert (plan.tile_m, plan.tile_n) == (tm, tn)
+            assert np.array_equal(bits(C), want), (tm, tn, split)
+
+
+def _suite():
+    with open(os.path.join(GOLDEN, "suite_gemm_s3.json")) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("op", _suite()["gemm"], ids=lambda o: o["name"])
+def test_reference_suite_hashes_gpu(torch_gpu, op):
+    """The 21 GEMMs of the reference's GPT-2 suite at 1024 tokens, S=3: the GPU output
+    hash equals the hash the reference recorded on every CPU and GPU it ran on."""
+    torch = torch_gpu
+    M, N, K = op["M"], op["N"], op["K"]
+    A = O.gen_normal(M * K, op["sa"], op["seed"])
+    B = O.gen_normal(K * N, op["sb"], op["seed"] + 1)
+    assert "%016x" % O.fnv_chain(A, B) == op["in_hash"]
+    note("suite op", op["name"])
+    C, _, _ = run(torch, A, B, M, N, K, rg.Config(trans_a=op["ta"], trans_b=op["tb"]))
+    assert "%016x" % O.fnv1a64(C.cpu().numpy()) == op["out_hash"]
+
+
+def test_reference_conv_hashes_gpu(torch_gpu):
+    """LeNet conv forward / weight gradient of the suite as GEMMs on im2col (K up to 78400)."""
+    from test_oracle import conv_gemm_cases, conv_post
+
+    torch = torch_gpu
+    for case in conv_gemm_cases():
+        note("conv", case["name"])
+        cfg = rg.Config(trans_a=case["ta"], trans_b=case["tb"])
+        C, _, _ = run(torch, case["A"], case["B"], case["M"], case["N"], case["K"], cfg)
+        out = conv_post(C.cpu().numpy(), case["post"])
+        assert "%016x" % O.fnv1a64(out) == case["golden"]["out_hash"], case["name"]
+
+
+@pytest.mark.parametrize("S", [1, 2, 3])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_slicing_kernel_digits_and_exponents(torch_gpu, S, ta, tb):
+    """Stage check of the slice split: the digit panels in the workspace recombine to the
+    oracle's fixed-point integers, digits stay in range, exponents equal the oracle's,
+    and padding is zero."""
+    torch = torch_gpu
+    M, N, K = 97, 70, 203
+    rng = np.random.default_rng(S * 4 + ta * 2 + tb)
+    A = (rng.standard_normal(M * K) * 2.0 ** rng.integers(-30, 30, M * K)).astype(np.float32)
+    B = rng.standard_normal(N * K).astype(np.float32)
+    A[:K] = 0.0                        # a zero row (or part of a column when ta)
+    A[K:2 * K] *= np.float32(2.0 ** -130)  # subnormal values
+    X, Y, eA, eB = O.quantize(A, B, M, N, K, ta, tb, S)
+    cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb, split_k=2)
+    note("slice S=%d ta=%d tb=%d" % (S, ta, tb))
+    C, plan, ws = run(torch, A, B, M, N, K, cfg)
+    info = rg.workspace_layout(M, N, K, cfg)
+    w = ws.cpu().numpy()
+    for off, R, Xo, eo, eoff in ((info.qa, info.Mp, X, eA, info.ea), (info.qb, info.Np, Y, eB, info.eb)):
+        d, Xg = decode_digits(w, off, R, info.Kp, S)
+        assert np.abs(d[0]).max() <= 127
+        if S > 1:
+            assert d[1:].min() >= -64 and d[1:].max() <= 63
+        assert np.array_equal(Xg[:Xo.shape[0], :K], Xo)
+        assert not Xg[Xo.shape[0]:].any() and not Xg[:, K:].any()
+        e = w[eoff:eoff + 4 * R].view(np.int32)
+        assert np.array_equal(e[:Xo.shape[0]], eo)
+        assert not e[Xo.shape[0]:].any()
+
+
+@pytest.mark.parametrize("split", [2, 3])
+def test_contraction_exact_products(torch_gpu, split):
+    """Stage check of the contraction: the int64 split-K partials sum to the exact
+    integer products T = X Y^T of the oracle."""
+    torch = torch_gpu
+    M, N, K = 130, 66, 1000
+    A = O.gen_normal(M * K, 1.0, 77)
+    B = O.gen_normal(N * K, 1.0, 78)
+    X, Y, _, _ = O.quantize(A, B, M, N, K, 0, 1, 3)
+    T = O.exact_products(X, Y)
+    for algo in (rg.Algo.TensorCore, rg.Algo.Tiled, rg.Algo.Reference):
+        cfg = rg.Config(algo=algo, split_k=split, trans_b=True)
+        note("products algo=%s split=%d" % (algo.name, split))
+        C, plan, ws = run(torch, A, B, M, N, K, cfg)
+        info = rg.workspace_layout(M, N, K, cfg)
+        part = ws.cpu().numpy()[info.part:info.part + 8 * plan.split_k * M * N].view(np.int64)
+        assert np.array_equal(part.reshape(plan.split_k, M, N).sum(axis=0), T)
+
+
+def test_stress_and_extreme_values(torch_gpu):
+    """hash_repro_gemm's stress pattern (zero, subnormal, 1e30, outlier and signed-zero
+    rows; zero, wide and tiny columns) plus results that overflow to +-inf and round to -0."""
+    from test_oracle import _stress_inputs
+
+    torch = torch_gpu
+    rng = np.random.default_rng(9)
+    M, N, K = 96, 60, 257
+    A, B = _stress_inputs(M, N, K, rng)
+    A[7] = np.float32(3e38)
+    B[:, 5] = np.float32(2e38)     # row 7 x column 5 overflows
+    A[11] = np.float32(-1e-45)
+    B[:, 8] = np.float32(1e-45)    # tiny negative products round to -0.0
+    for S in (1, 2, 3):
+        want = O.cpu_gemm(A, B, M, N, K, 0, 0, S).view(np.uint32)
+        for algo in ALGOS[:3]:
+            note("stress S=%d %s" % (S, algo.name))
+            C, _, _ = run(torch, A, B, M, N, K, rg.Config(algo=algo, slices=S))
+            assert np.array_equal(bits(C), want)
+    assert np.isinf(O.cpu_gemm(A, B, M, N, K, 0, 0, 3)[7, 5])
+
+
+def test_stage_events_and_streams(torch_gpu):
+    torch = torch_gpu
+    M, N, K = 512, 512, 1024
+    A = O.gen_normal(M * K, 1.0, 5)
+    B = O.gen_normal(K * N, 1.0, 6)
+    want = O.cpu_gemm(A, B, M, N, K, 0, 0, 3).view(np.uint32)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dA, dB = to_dev(torch, A), to_dev(torch, B)
+        C, _, _ = run(torch, dA, dB, M, N, K, rg.Config(split_k=3),
+                      events=[e.cuda_event for e in ev], stream=s.cuda_stream)
+    s.synchronize()
+    times = [ev[0].elapsed_time(ev[i]) for i in (1, 2, 3)]
+    assert 0 <= times[0] <= times[1] <= times[2]
+    assert np.array_equal(bits(C), want)
+
+
+def test_error_codes_on_device(torch_gpu):
+    torch = torch_gpu
+    M = N = K = 64
+    dA = torch.zeros(M * K, device="cuda")
+    dC = torch.zeros(M * N, device="cuda")
+    plan = rg.make_plan(M, N, K, rg.Config())
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    cfg = rg.Config()
+    assert rg.repro_gemm_fp32_ws(dA.data_ptr(), dA.data_ptr(), dC.data_ptr(), M, N, K, cfg,
+                                 ws.data_ptr(), plan.workspace_bytes - 1) == 1
+    assert rg.repro_gemm_fp32_ws(dA.data_ptr(), dA.data_ptr(), dC.data_ptr(), M, N, K,
+                                 rg.Config(slices=4), ws.data_ptr(), ws.numel()) == 1
+    assert rg.repro_gemm_fp32(dA.data_ptr(), dA.data_ptr(), dC.data_ptr(), M, N, K, cfg) == 0
+    assert rg.repro_gemm_fp32(dA.data_ptr(), dA.data_ptr(), dC.data_ptr(), 0, N, K, cfg) == 1
+
+
+def test_torch_gemm_binding(torch_gpu):
+    """rg.gemm mirrors repro_torch's _backend.gemm: Linear forward, dX and dW."""
+    torch = torch_gpu
+    B_, fin, fout = 64, 400, 120
+    X = O.gen_normal(B_ * fin, 1.0, 1)
+    W = O.gen_normal(fout * fin, 0.05, 2)
+    dY = O.gen_normal(B_ * fout, 1.0, 3)
+    tX, tW, tdY = (torch.from_numpy(v).cuda() for v in (X, W, dY))
+    Y = rg.gemm(tX.view(B_, fin), tW.view(fout, fin), B_, fout, fin, False, True, 3)
+    dX = rg.gemm(tdY, tW, B_, fin, fout, False, False, 3)
+    dW = rg.gemm(tdY, tX, fout, fin, B_, True, False, 3)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(Y), O.cpu_gemm(X, W, B_, fout, fin, 0, 1, 3).view(np.uint32))
+    assert np.array_equal(bits(dX), O.cpu_gemm(dY, W, B_, fin, fout, 0, 0, 3).view(np.uint32))
+    assert np.array_equal(bits(dW), O.cpu_gemm(dY, X, fout, fin, B_, 1, 0, 3).view(np.uint32))
+    # non-contiguous input is made contiguous, like the reference binding
+    Wt = torch.from_numpy(W.reshape(fout, fin).T.copy()).cuda().t()
+    Y2 = rg.gemm(tX, Wt, B_, fout, fin, False, True, 3)
+    assert torch.equal(Y2.view(torch.int32), Y.view(torch.int32))
+    with pytest.raises(ValueError):
+        rg.gemm(torch.from_numpy(X), torch.from_numpy(W), B_, fout, fin, False, True, 3)

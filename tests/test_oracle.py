@@ -1,0 +1,359 @@
+"""Pins the CPU oracle (oracle/repro_oracle.c) before anything is checked against it.
+
+Each check is independent of the oracle's own formulas: published test vectors, exact
+rational arithmetic (tests/exact.py), an integer formulation of the division, brute force
+with Python integers, the reference's recorded suite hashes, and the reference's own CPU
+path compiled from its headers (oracle/_ref) where that is built.
+"""
+import json
+import os
+import random
+
+import numpy as np
+import pytest
+
+import exact
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---------------------------------------------------------------------------------------
+# Hash and generator
+# ---------------------------------------------------------------------------------------
+
+def test_fnv1a64_published_vectors():
+    # FNV-1a 64-bit test vectors (Fowler/Noll/Vo reference set).
+    assert O.fnv1a64(np.frombuffer(b"", np.uint8)) == 0xCBF29CE484222325
+    assert O.fnv1a64(np.frombuffer(b"a", np.uint8)) == 0xAF63DC4C8601EC8C
+    assert O.fnv1a64(np.frombuffer(b"foobar", np.uint8)) == 0x85944171F73967E8
+
+
+def _py_splitmix(seed, n):
+    mask = (1 << 64) - 1
+    s = seed & mask
+    out = []
+    for _ in range(n):
+        s = (s + 0x9E3779B97F4A7C15) & mask
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        out.append(z ^ (z >> 31))
+    return out
+
+
+def test_splitmix64_known_answer_and_python():
+    # SplitMix64 seeded with 0 (Vigna's reference implementation): first output.
+    assert int(O.splitmix64(1, 0)[0]) == 0xE220A8397B1DCDAF
+    for seed in (0, 1, 12345, 2 ** 63 + 7):
+        assert [int(v) for v in O.splitmix64(50, seed)] == _py_splitmix(seed, 50)
+
+
+def test_gen_normal_matches_python_irwin_hall():
+    seed = 777
+    draws = _py_splitmix(seed, 12 * 40)
+    want = []
+    for i in range(40):
+        t = sum((d >> 40) * (1.0 / 16777216.0) for d in draws[12 * i:12 * i + 12])
+        want.append(np.float32(0.5 * (t - 6.0)))
+    got = O.gen_normal(40, 0.5, seed)
+    assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
+    # Continuing the stream at element 17 equals the tail of one long draw.
+    assert np.array_equal(O.gen_normal(23, 0.5, seed, first=17), got[17:])
+
+
+def test_gen_uniform_pm_matches_reference_recipe():
+    # repro_torch/utils.py:23-29 in float32 numpy arithmetic.
+    seed, n = 99, 64
+    bound = np.float32(1.0) / np.sqrt(np.float32(120))
+    bits = np.array([d >> 40 for d in _py_splitmix(seed, n)], dtype=np.float32)
+    u = bits * np.float32(2.0 ** -24)
+    want = (u * (np.float32(2.0) * bound)) - bound
+    got = O.gen_uniform_pm(n, float(bound), seed)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------
+# Scalars
+# ---------------------------------------------------------------------------------------
+
+def test_scale_exponent_exhaustive_integer_formulation():
+    """Every non-negative finite float: division-based definition == integer division
+    with round-to-nearest-even (written separately inside the oracle's test hook)."""
+    bad, first = O.check_scale_exponent_range(0, 0x7F800000)
+    assert bad == 0, "first mismatch at bits %08x" % first
+
+
+def _edge_floats():
+    vals = [0.0, -0.0, 1.0, 127.0, 126.99999, 127.00001, 254.0, 1e-45, 2e-45, 1e-40, 1.1754942e-38,
+            1.1754944e-38, 3.4028235e38, 1e30, 1e-30, 0.5, 63.5 * 2.0 ** -149]
+    rng = random.Random(5)
+    for _ in range(300):
+        b = rng.randrange(0, 0x7F800000)
+        vals.append(float(exact.bits_f32(b)))
+    for e in range(-149, 128, 3):  # powers of two and 127 * 2^e neighbourhoods
+        for m in (1.0, 127.0, 127.0 * (1 + 2 ** -23), 127.0 * (1 - 2 ** -24)):
+            v = np.float32(m * 2.0 ** e)
+            if np.isfinite(v):
+                vals.append(float(v))
+    return np.array(vals, np.float32)
+
+
+def test_scale_exponent_exact_rational():
+    m = _edge_floats()
+    got = O.scale_exponent_n(m)
+    want = [exact.scale_exponent(v) for v in m]
+    assert list(got) == want
+
+
+def test_scale_exponent_closed_forms():
+    # m = 127 * 2^e exactly -> e (fl(m/127) = 2^e); m = 1 -> smallest e with 2^e >= 1/127 = -6.
+    for e in range(-120, 120, 7):
+        assert O.lib.oracle_scale_exponent(np.float32(127.0 * 2.0 ** e)) == e
+    assert O.lib.oracle_scale_exponent(1.0) == -6
+    assert O.lib.oracle_scale_exponent(0.0) == 0
+    assert O.lib.oracle_scale_exponent(-5.0) == 0
+    # The smallest subnormals divided by 127 round to zero -> exponent 0.
+    assert O.lib.oracle_scale_exponent(float(exact.bits_f32(1))) == 0
+
+
+@pytest.mark.parametrize("S", [1, 2, 3])
+def test_fixed_point_exact_rational(S):
+    rng = random.Random(10 + S)
+    xs, ses = [], []
+    for _ in range(1500):
+        se = rng.randint(-149, 127)
+        kind = rng.random()
+        if kind < 0.5:   # values within the row scale
+            x = rng.uniform(-127, 127) * 2.0 ** se
+        elif kind < 0.7:  # exact ties after scaling: (n + 1/2) * 2^(se - 7(S-1))
+            x = (rng.randint(-2 ** 20, 2 ** 20) + 0.5) * 2.0 ** (se - 7 * (S - 1))
+        elif kind < 0.85:  # subnormal inputs
+            x = float(exact.bits_f32(rng.randrange(1, 0x800000))) * rng.choice((-1, 1))
+        else:  # beyond the clamp
+            x = rng.uniform(127, 200) * 2.0 ** se * rng.choice((-1, 1))
+        x = np.float32(x)
+        if not np.isfinite(x):
+            continue
+        # Reachable domain: the row exponent comes from a row max >= |x|.
+        se = max(se, int(O.lib.oracle_scale_exponent(float(abs(x)))))
+        xs.append(x)
+        ses.append(se)
+    xs = np.array(xs, np.float32)
+    got = O.fixed_point_n(xs, np.array(ses, np.int32), S)
+    want = [exact.fixed_point(x, se, S) for x, se in zip(xs, ses)]
+    assert list(got) == want
+
+
+def _round_cases():
+    rng = random.Random(3)
+    T, E = [], []
+    for _ in range(3000):
+        kind = rng.random()
+        if kind < 0.4:
+            t = rng.randint(-2 ** 62, 2 ** 62)
+            e = rng.randint(-330, 220)
+        elif kind < 0.6:  # ties: odd multiple of half an ulp
+            q = rng.randint(2 ** 23, 2 ** 24 - 1)
+            sh = rng.randint(1, 38)
+            t = (2 * q + 1) << (sh - 1)
+            t *= rng.choice((-1, 1))
+            e = rng.randint(-200, 100) - sh
+        elif kind < 0.8:  # subnormal boundary: |T| * 2^E near 2^-149 .. 2^-126
+            t = rng.randint(1, 2 ** 40) * rng.choice((-1, 1))
+            e = -149 - t.bit_length() + rng.randint(-3, 26)
+        else:  # overflow boundary near 2^128
+            t = rng.randint(2 ** 40, 2 ** 62) * rng.choice((-1, 1))
+            e = 128 - t.bit_length() + rng.randint(-2, 1)
+        T.append(t)
+        E.append(e)
+    T += [0, 1, -1, 2 ** 62, -(2 ** 62), 2 ** 24 + 1, -(2 ** 24 + 1), 3]
+    E += [0, -150, -150, 66, 66, -10, -10, -151]
+    return np.array(T, np.int64), np.array(E, np.int32)
+
+
+def test_round_to_float_exact_rational():
+    T, E = _round_cases()
+    got = O.round_to_float_n(T, E).view(np.uint32)
+    want = [exact.round_to_float_bits(t, e) for t, e in zip(T.tolist(), E.tolist())]
+    assert [int(g) for g in got] == want
+
+
+def test_round_to_float_special_values():
+    f = O.lib.oracle_round_to_float
+    assert exact.f32_bits(f(0, 5)) == 0x00000000
+    assert exact.f32_bits(f(-1, -151)) == 0x80000000      # negative, rounds to zero: -0.0
+    assert exact.f32_bits(f(1, -149)) == 0x00000001       # smallest subnormal
+    assert exact.f32_bits(f(1, -150)) == 0x00000000       # tie to even -> 0
+    assert exact.f32_bits(f(3, -150)) == 0x00000002       # 1.5 ulp -> 2 ulp
+    assert exact.f32_bits(f(1, 128)) == 0x7F800000        # overflow
+    assert exact.f32_bits(f(-(2 ** 24 - 1), 104)) == 0xFF7FFFFF  # -FLT_MAX
+
+
+# ---------------------------------------------------------------------------------------
+# Whole GEMM
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("S", [1, 2, 3])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_cpu_gemm_brute_force(S, ta, tb):
+    rng = np.random.default_rng(100 + 10 * S + 2 * ta + tb)
+    M, N, K = 5, 4, 9
+    A = (rng.standard_normal(M * K) * 2.0 ** rng.integers(-20, 20, M * K)).astype(np.float32)
+    B = (rng.standard_normal(K * N) * 2.0 ** rng.integers(-20, 20, K * N)).astype(np.float32)
+    A[3] = 0.0
+    B[::7] = np.float32(1e-42)  # subnormals
+    C = O.cpu_gemm(A, B, M, N, K, ta, tb, S)
+    assert np.array_equal(C.view(np.uint32), exact.gemm_bits(A, B, M, N, K, ta, tb, S))
+
+
+def _suite():
+    with open(os.path.join(GOLDEN, "suite_gemm_s3.json")) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("op", _suite()["gemm"], ids=lambda o: o["name"])
+def test_reference_suite_hashes(op):
+    """The reference's recorded GPT-2 suite GEMMs (1024 tokens, S=3): input and output
+    FNV-1a-64 hashes (gpt2_ops_suite/results/mac/cpu.txt:2-22)."""
+    M, N, K = op["M"], op["N"], op["K"]
+    A = O.gen_normal(M * K, op["sa"], op["seed"])
+    B = O.gen_normal(K * N, op["sb"], op["seed"] + 1)
+    assert "%016x" % O.fnv_chain(A, B) == op["in_hash"]
+    C = O.cpu_gemm(A, B, M, N, K, op["ta"], op["tb"], 3)
+    assert "%016x" % O.fnv1a64(C) == op["out_hash"]
+
+
+def im2col(x, Nimg, Cin, H, W, KH, KW, P):
+    """X[w][k] for windows w = (n, oy, ox) and positions k = (c, ky, kx), stride 1,
+    zero padding P (repro_conv_cuda/repro_conv_math.cuh:43-66)."""
+    x = x.reshape(Nimg, Cin, H, W)
+    xp = np.pad(x, ((0, 0), (0, 0), (P, P), (P, P)))
+    OH, OW = H + 2 * P - KH + 1, W + 2 * P - KW + 1
+    cols = np.empty((Nimg, OH, OW, Cin, KH, KW), np.float32)
+    for ky in range(KH):
+        for kx in range(KW):
+            cols[:, :, :, :, ky, kx] = xp[:, :, ky:ky + OH, kx:kx + OW].transpose(0, 2, 3, 1)
+    return cols.reshape(Nimg * OH * OW, Cin * KH * KW), OH, OW
+
+
+CONV = {
+    "lenet conv1": dict(N=100, C=1, H=28, W=28, F=6, KH=5, KW=5, P=2, seed_fwd=1340, seed_dw=1350),
+    "lenet conv2": dict(N=100, C=6, H=14, W=14, F=16, KH=5, KW=5, P=0, seed_fwd=1360, seed_dw=1370),
+}
+
+
+def conv_gemm_cases():
+    """The suite's LeNet convolution forward and weight gradient as GEMMs on im2col
+    (repro_conv_cuda/test_repro_conv.cu:84-112): forward Y = X W^T then [W][F] -> NCHW,
+    weight gradient dW = dY^T X. Inputs per gpt2_ops_suite.cu:432-436."""
+    golden = _suite()["conv"]
+    out = []
+    for name, g in CONV.items():
+        K = g["C"] * g["KH"] * g["KW"]
+        x = O.gen_normal(g["N"] * g["C"] * g["H"] * g["W"], 1.0, g["seed_fwd"])
+        w = O.gen_normal(g["F"] * K, 0.1, g["seed_fwd"] + 1)
+        X, OH, OW = im2col(x, g["N"], g["C"], g["H"], g["W"], g["KH"], g["KW"], g["P"])
+        Wn = X.shape[0]
+        out.append(dict(name=name + ".fwd", inputs=(x, w), A=X, B=w, M=Wn, N=g["F"], K=K, ta=0,
+                        tb=1, post=("nchw", g["N"], g["F"], OH, OW), golden=golden[name + ".fwd"]))
+        xd = O.gen_normal(g["N"] * g["C"] * g["H"] * g["W"], 1.0, g["seed_dw"])
+        dy = O.gen_normal(g["N"] * g["F"] * OH * OW, 1e-3, g["seed_dw"] + 2)
+        Xd, _, _ = im2col(xd, g["N"], g["C"], g["H"], g["W"], g["KH"], g["KW"], g["P"])
+        D = dy.reshape(g["N"], g["F"], OH, OW).transpose(0, 2, 3, 1).reshape(Wn, g["F"])
+        out.append(dict(name=name + ".dW", inputs=(dy, xd), A=np.ascontiguousarray(D), B=Xd,
+                        M=g["F"], N=K, K=Wn, ta=1, tb=0, post=None, golden=golden[name + ".dW"]))
+    return out
+
+
+def conv_post(C, post):
+    if post is None:
+        return C
+    _, n, f, oh, ow = post
+    return np.ascontiguousarray(C.reshape(n, oh, ow, f).transpose(0, 3, 1, 2))
+
+
+def test_reference_conv_hashes():
+    """LeNet conv forward and weight gradient of the suite (cpu.txt:35-38) through the
+    GEMM definition on im2col: pins the transposed-A path with K = 78400."""
+    for case in conv_gemm_cases():
+        assert "%016x" % O.fnv_chain(*case["inputs"]) == case["golden"]["in_hash"], case["name"]
+        C = O.cpu_gemm(case["A"], case["B"], case["M"], case["N"], case["K"], case["ta"],
+                       case["tb"], 3)
+        assert "%016x" % O.fnv1a64(conv_post(C, case["post"])) == case["golden"]["out_hash"], \
+            case["name"]
+
+
+def _stress_inputs(M, N, K, rng):
+    """hash_repro_gemm's 'stress' pattern (repro_gemm_cuda/hash_repro_gemm.cu:32-56)
+    restated: zero, subnormal, 1e30-scale, outlier and signed-zero rows; zero, wide and
+    tiny columns."""
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    for r in range(M):
+        kind = r % 8
+        if kind == 1:
+            A[r] = 0.0
+        elif kind == 2:
+            A[r] = (rng.standard_normal(K) * 2.0 ** -140).astype(np.float32)
+        elif kind == 3:
+            A[r] = (rng.standard_normal(K) * 1e30).astype(np.float32)
+        elif kind == 4:
+            A[r, rng.integers(K)] = 1e6
+        elif kind == 5:
+            A[r] = np.where(np.arange(K) % 2 == 1, np.float32(-0.0), np.float32(0.0))
+    for c in range(N):
+        kind = c % 6
+        if kind == 1:
+            B[:, c] = 0.0
+        elif kind == 2:
+            B[:, c] = (np.sign(rng.standard_normal(K)) * 2.0 ** rng.integers(-60, 61, K)).astype(np.float32)
+        elif kind == 3:
+            B[:, c] = (rng.standard_normal(K) * 2.0 ** -120).astype(np.float32)
+    return A, B
+
+
+@pytest.mark.skipif(O.ref is None, reason="reference CPU path (oracle/_ref) not built here")
+@pytest.mark.parametrize("S", [1, 2, 3])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("dist", ["normal", "stress"])
+def test_oracle_matches_reference_cpu_path(S, ta, tb, dist):
+    """S=1/2, the (1,1) transpose and the stress distribution have no recorded hash;
+    the reference's own CPU path pins them."""
+    rng = np.random.default_rng(7 * S + 3 * ta + tb)
+    M, N, K = 67, 45, 301
+    if dist == "normal":
+        A = rng.standard_normal(M * K).astype(np.float32)
+        B = rng.standard_normal(K * N).astype(np.float32)
+    else:
+        A, B = _stress_inputs(M, N, K, rng)
+        if ta:
+            A = np.ascontiguousarray(A.T)
+        if tb:
+            B = np.ascontiguousarray(B.T)
+    C = O.cpu_gemm(A, B, M, N, K, ta, tb, S)
+    R = O.ref_cpu_gemm(A, B, M, N, K, ta, tb, S)
+    assert np.array_equal(C.view(np.uint32), R.view(np.uint32))
+
+
+@pytest.mark.skipif(O.ref is None, reason="reference CPU path (oracle/_ref) not built here")
+def test_oracle_scalars_match_reference_header():
+    m = _edge_floats()
+    assert [O.ref.ref_scale_exponent(float(v)) for v in m] == list(O.scale_exponent_n(m))
+    T, E = _round_cases()
+    want = [exact.f32_bits(O.ref.ref_round_to_float(int(t), int(e))) for t, e in zip(T, E)]
+    assert [int(b) for b in O.round_to_float_n(T, E).view(np.uint32)] == want
+
+
+def test_baseline_fixtures_small_configs():
+    """Re-derives the committed fixtures of configs 1 and 2 with the oracle."""
+    from golden import configs
+
+    with open(os.path.join(GOLDEN, "baseline_configs.json")) as f:
+        fx = {c["name"]: c for c in json.load(f)["cases"]}
+    for case in configs.config1() + configs.config2():
+        A, B = case["make"]()
+        row = fx[case["name"]]
+        assert "%016x" % O.fnv_chain(A, B) == row["in_hash"]
+        C = O.cpu_gemm(A, B, case["M"], case["N"], case["K"], case["ta"], case["tb"], case["S"])
+        assert "%016x" % O.fnv1a64(C) == row["out_hash"]
