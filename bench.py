@@ -160,6 +160,8 @@ def main():
     # Timed region: exactly `steps` GEMMs; stage events on the launch stream give the
     # contraction kernel's own duration (event 1 -> event 2 brackets only that launch).
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for e in (x for row in evs for x in row):
+        e.record(stream)  # torch creates the HIP event on first record
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):

@@ -79,7 +79,37 @@ _SIGNATURES = {
 EXPORTED = tuple(_SIGNATURES)
 
 
+def _bind_after_torch():
+    """Makes the library use the same HIP runtime as PyTorch.
+
+    torch bundles its own libamdhip64 (SONAME libamdhip64.so.7, requested by libtorch_hip
+    as plain "libamdhip64.so" from torch/lib). If librepro_gemm.so were loaded first, the
+    dynamic loader would bind the system runtime, and a later `import torch` would map a
+    second HIP runtime into the process, which breaks both. Importing torch first lets the
+    loader resolve this library's libamdhip64.so.7 to torch's already-loaded copy.
+    Set RG_NO_TORCH=1 in processes that never use torch to skip the import.
+    """
+    if os.environ.get("RG_NO_TORCH") == "1":
+        return
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
+def hip_runtimes_mapped():
+    """Paths of every libamdhip64 mapped into this process (should be exactly one)."""
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64" in os.path.basename(parts[5]):
+                paths.add(os.path.realpath(parts[5]))
+    return sorted(paths)
+
+
 def _load():
+    _bind_after_torch()
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             "librepro_gemm.so is not built (%s); run __graft_entry__.build() or "

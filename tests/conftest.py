@@ -33,6 +33,11 @@ _ensure_built()
 def torch_gpu():
     import torch
 
+    from bit_reproducible_training_amd import _lib
+
     if not torch.cuda.is_available():
         pytest.fail("GPU test requested but torch.cuda is not available")
+    runtimes = _lib.hip_runtimes_mapped()
+    print("HIP runtime(s) mapped:", runtimes, flush=True)
+    assert len(runtimes) == 1, "two HIP runtimes in one process: %s" % runtimes
     return torch

@@ -38,6 +38,15 @@ def run(torch, A, B, M, N, K, cfg, ws=None, poison=True, events=None, stream=Non
     return C, plan, ws
 
 
+def hip_events(torch, n, stream=None):
+    """n timing events whose HIP handles exist (torch creates them on first record)."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for e in evs:
+        e.record(stream) if stream is not None else e.record()
+    torch.cuda.synchronize()
+    return evs
+
+
 def bits(C):
     return C.cpu().numpy().view(np.uint32)
 

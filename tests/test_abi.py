@@ -28,6 +28,13 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(_lib.EXPORTED)
 
 
+def test_single_hip_runtime_in_process():
+    """The library and torch share one HIP runtime (two in one process crash)."""
+    import torch  # noqa: F401
+
+    assert len(_lib.hip_runtimes_mapped()) == 1, _lib.hip_runtimes_mapped()
+
+
 def test_config_defaults_match_reference():
     c = _lib.rg_config()
     _lib.lib.rg_config_init(ctypes.byref(c))

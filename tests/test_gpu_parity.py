@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import bit_reproducible_training_amd as rg
-from gpu_util import bits, decode_digits, note, run, to_dev
+from gpu_util import bits, decode_digits, hip_events, note, run, to_dev
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -192,8 +192,8 @@ def test_stage_events_and_streams(torch_gpu):
     A = O.gen_normal(M * K, 1.0, 5)
     B = O.gen_normal(K * N, 1.0, 6)
     want = O.cpu_gemm(A, B, M, N, K, 0, 0, 3).view(np.uint32)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     s = torch.cuda.Stream()
+    ev = hip_events(torch, 4, s)
     with torch.cuda.stream(s):
         dA, dB = to_dev(torch, A), to_dev(torch, B)
         C, _, _ = run(torch, dA, dB, M, N, K, rg.Config(split_k=3),
