@@ -25,23 +25,24 @@ using repro_gemm::round_to_float;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-template <int S, int TI, int TJ>
-__global__ void __launch_bounds__(256, 1)
+template <int S, int WTI, int WTJ, int WGM, int WGN>
+__global__ void __launch_bounds__(64 * WGM * WGN)
 contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
               const int* __restrict__ eA, const int* __restrict__ eB, float* __restrict__ C,
               int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n) {
     constexpr int L = 2 * S - 1;
-    constexpr int BM = 64 * TI, BN = 64 * TJ;
+    constexpr int NW = WGM * WGN;                  // wavefronts per block
+    constexpr int BM = WGM * WTI * 32, BN = WGN * WTJ * 32;
     constexpr int PA = (BM / PANEL_ROWS) * 2 * S;  // A panels per stage
     constexpr int PB = (BN / PANEL_ROWS) * 2 * S;  // B panels per stage
     constexpr int PT = PA + PB;
-    constexpr int PW = PT / 4;                     // panels copied per wavefront per stage
-    static_assert(PT % 4 == 0, "stage panels must split evenly over 4 wavefronts");
+    constexpr int PW = PT / NW;                    // panels copied per wavefront per stage
+    static_assert(PT % NW == 0, "stage panels must split evenly over the wavefronts");
     __shared__ v4i lds[2][PT][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
     const int part = blockIdx.y;
     const int nsteps = Kp / STEP_K;
@@ -50,39 +51,40 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     const size_t row_stride = (size_t)(Kp / PANEL_K) * S * (PANEL_BYTES / 16);  // in v4i
     const size_t step_stride = (size_t)2 * S * (PANEL_BYTES / 16);              // in v4i
 
-    // Source of each panel this wavefront copies, at step 0.
-    const v4i* src[PW];
+    // Source of each panel this wavefront copies, at step 0 (wavefront-uniform offsets).
+    size_t soff[PW];
+    const v4i* sbase[PW];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-        const int pi = wave + 4 * i;
+        const int pi = wave + NW * i;
         if (pi < PA) {
             const int rl = pi / (2 * S), o = pi % (2 * S);
-            src[i] = reinterpret_cast<const v4i*>(QA) + (size_t)(tm * (BM / PANEL_ROWS) + rl) * row_stride +
-                     (size_t)o * (PANEL_BYTES / 16) + lane;
+            sbase[i] = reinterpret_cast<const v4i*>(QA);
+            soff[i] = (size_t)(tm * (BM / PANEL_ROWS) + rl) * row_stride + (size_t)o * (PANEL_BYTES / 16);
         } else {
             const int pb = pi - PA;
             const int cl = pb / (2 * S), o = pb % (2 * S);
-            src[i] = reinterpret_cast<const v4i*>(QB) + (size_t)(tn * (BN / PANEL_ROWS) + cl) * row_stride +
-                     (size_t)o * (PANEL_BYTES / 16) + lane;
+            sbase[i] = reinterpret_cast<const v4i*>(QB);
+            soff[i] = (size_t)(tn * (BN / PANEL_ROWS) + cl) * row_stride + (size_t)o * (PANEL_BYTES / 16);
         }
     }
 
-    v16i acc[L][TI][TJ];
+    v16i acc[L][WTI][WTJ];
 #pragma unroll
     for (int l = 0; l < L; ++l)
 #pragma unroll
-        for (int ti = 0; ti < TI; ++ti)
+        for (int ti = 0; ti < WTI; ++ti)
 #pragma unroll
-            for (int tj = 0; tj < TJ; ++tj)
+            for (int tj = 0; tj < WTJ; ++tj)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[l][ti][tj][e] = 0;
 
     v4i stage[PW];
     if (s0 < s1) {
 #pragma unroll
-        for (int i = 0; i < PW; ++i) stage[i] = src[i][(size_t)s0 * step_stride];
+        for (int i = 0; i < PW; ++i) stage[i] = sbase[i][soff[i] + (size_t)s0 * step_stride + lane];
 #pragma unroll
-        for (int i = 0; i < PW; ++i) lds[0][wave + 4 * i][lane] = stage[i];
+        for (int i = 0; i < PW; ++i) lds[0][wave + NW * i][lane] = stage[i];
     }
     __syncthreads();
 
@@ -91,32 +93,33 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
         const bool more = s + 1 < s1;
         if (more) {
 #pragma unroll
-            for (int i = 0; i < PW; ++i) stage[i] = src[i][(size_t)(s + 1) * step_stride];
+            for (int i = 0; i < PW; ++i)
+                stage[i] = sbase[i][soff[i] + (size_t)(s + 1) * step_stride + lane];
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            v4i a[S][TI], b[S][TJ];
+            v4i a[S][WTI], b[S][WTJ];
 #pragma unroll
             for (int p = 0; p < S; ++p) {
 #pragma unroll
-                for (int ti = 0; ti < TI; ++ti) a[p][ti] = lds[cur][((wm * TI + ti) * 2 + kk) * S + p][lane];
+                for (int ti = 0; ti < WTI; ++ti) a[p][ti] = lds[cur][((wm * WTI + ti) * 2 + kk) * S + p][lane];
 #pragma unroll
-                for (int tj = 0; tj < TJ; ++tj) b[p][tj] = lds[cur][PA + ((wn * TJ + tj) * 2 + kk) * S + p][lane];
+                for (int tj = 0; tj < WTJ; ++tj) b[p][tj] = lds[cur][PA + ((wn * WTJ + tj) * 2 + kk) * S + p][lane];
             }
 #pragma unroll
             for (int p = 0; p < S; ++p)
 #pragma unroll
                 for (int q = 0; q < S; ++q)
 #pragma unroll
-                    for (int ti = 0; ti < TI; ++ti)
+                    for (int ti = 0; ti < WTI; ++ti)
 #pragma unroll
-                        for (int tj = 0; tj < TJ; ++tj)
+                        for (int tj = 0; tj < WTJ; ++tj)
                             acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
                                 a[p][ti], b[q][tj], acc[p + q][ti][tj], 0, 0, 0);
         }
         if (more) {
 #pragma unroll
-            for (int i = 0; i < PW; ++i) lds[cur ^ 1][wave + 4 * i][lane] = stage[i];
+            for (int i = 0; i < PW; ++i) lds[cur ^ 1][wave + NW * i][lane] = stage[i];
         }
         __syncthreads();
     }
@@ -125,24 +128,26 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // column lane%32.
     const int e0 = -14 * (S - 1);
 #pragma unroll
-    for (int ti = 0; ti < TI; ++ti) {
+    for (int ti = 0; ti < WTI; ++ti) {
 #pragma unroll
-        for (int tj = 0; tj < TJ; ++tj) {
-            const int rbase = tm * BM + (wm * TI + ti) * 32 + 4 * (lane >> 5);
-            const int col = tn * BN + (wn * TJ + tj) * 32 + (lane & 31);
-            if (col >= N) continue;
-            const int ec = eB[col] + e0;
+        for (int tj = 0; tj < WTJ; ++tj) {
+            const int rbase = tm * BM + (wm * WTI + ti) * 32 + 4 * (lane >> 5);
+            const int col = tn * BN + (wn * WTJ + tj) * 32 + (lane & 31);
+            if (col < N) {
+                const int ec = eB[col] + e0;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = rbase + 8 * (e >> 2) + (e & 3);
-                if (row >= M) continue;
-                int64_t t = 0;
+                for (int e = 0; e < 16; ++e) {
+                    const int row = rbase + 8 * (e >> 2) + (e & 3);
+                    if (row >= M) continue;
+                    int64_t t = 0;
 #pragma unroll
-                for (int l = 0; l < L; ++l) t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
-                if (split == 1)
-                    C[(size_t)row * N + col] = round_to_float(t, eA[row] + ec);
-                else
-                    partial[((size_t)part * M + row) * N + col] = t;
+                    for (int l = 0; l < L; ++l)
+                        t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
+                    if (split == 1)
+                        C[(size_t)row * N + col] = round_to_float(t, eA[row] + ec);
+                    else
+                        partial[((size_t)part * M + row) * N + col] = t;
+                }
             }
             // Keep the scheduler from hoisting every accumulator read to the top.
             __builtin_amdgcn_sched_barrier(0);
@@ -186,14 +191,15 @@ static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, c
                           const int* eb, float* C, int64_t* partial, hipStream_t stream) {
     const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)L.split);
+    // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64, 64x128, 64x64 = 4 wavefronts.
     if (L.ti == 2 && L.tj == 2)
-        contract_mfma<S, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 2, 1, 2, 4><<<grid, 512, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
     else if (L.ti == 2 && L.tj == 1)
-        contract_mfma<S, 2, 1><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 2, 1, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
     else if (L.ti == 1 && L.tj == 2)
-        contract_mfma<S, 1, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 1, 2, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
     else
-        contract_mfma<S, 1, 1><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 1, 1, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
 }
 
 void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
