@@ -42,17 +42,19 @@ int max_steps_per_part(int S) {
     return (int)(n / STEP_K);
 }
 
-// Row-max pass chunking: enough wavefronts to cover the GPU, at most 16 partials per row.
+// Row-max pass chunking, from shapes only (so the workspace size never depends on pointer
+// alignment): enough blocks to keep HBM busy, at most 16 (row access) or 32 (column access)
+// partial maxima per row, chunk lengths a multiple of 4 for float4 loads.
 void choose_chunks(int R, int K, bool strided, int* nch, int* kch) {
     int n;
     if (strided) {
-        int groups = ceil_div(R, 64);
-        n = std::min(ceil_div(2048, groups), std::min(16, ceil_div(K, 64)));
+        int groups = ceil_div(R, R % 4 == 0 ? 256 : 64);
+        n = std::min(ceil_div(1024, groups), std::min(32, ceil_div(K, 16)));
     } else {
         n = std::min(ceil_div(2048, R), std::min(16, ceil_div(K, 256)));
     }
     n = std::max(1, n);
-    *kch = ceil_div(K, n);
+    *kch = round_up(ceil_div(K, n), 4);
     *nch = ceil_div(K, *kch);
 }
 
@@ -270,11 +272,31 @@ int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int 
     int64_t* part = L.has_partial ? reinterpret_cast<int64_t*>(base + L.part) : nullptr;
     const bool i32 = L.algo == RG_ALGO_REFERENCE;
 
+    auto desc = [&](const float* src, int R, int Rp, bool strided, int nch, int kch, float* pm,
+                    void* out, int* expo) {
+        rg::SliceDesc d;
+        d.src = src;
+        d.R = R;
+        d.K = K;
+        d.Rp = Rp;
+        d.Kp = L.Kp;
+        d.strided = strided ? 1 : 0;
+        const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+        d.vec = aligned && (strided ? (R % 4 == 0) : (K % 4 == 0)) ? 1 : 0;
+        d.nch = nch;
+        d.kch = kch;
+        d.pmax = pm;
+        d.out = out;
+        d.expo = expo;
+        rg::slice_grid(d);
+        return d;
+    };
+    const rg::SliceDesc da = desc(A, M, L.Mp, L.a_strided, L.nch_a, L.kch_a, pma, qa, ea);
+    const rg::SliceDesc db = desc(B, N, L.Np, L.b_strided, L.nch_b, L.kch_b, pmb, qb, eb);
+
     record(0);
-    rg::launch_absmax(A, M, K, L.a_strided, L.nch_a, L.kch_a, L.Mp, pma, stream);
-    rg::launch_absmax(B, N, K, L.b_strided, L.nch_b, L.kch_b, L.Np, pmb, stream);
-    rg::launch_slice(A, M, K, L.Mp, L.Kp, L.a_strided, pma, L.nch_a, L.S, i32, qa, ea, stream);
-    rg::launch_slice(B, N, K, L.Np, L.Kp, L.b_strided, pmb, L.nch_b, L.S, i32, qb, eb, stream);
+    rg::launch_absmax(da, db, stream);
+    rg::launch_split(da, db, L.S, i32, stream);
     record(1);
     if (i32)
         rg::launch_contract_reference(L, static_cast<const int32_t*>(qa),

@@ -43,11 +43,26 @@ struct DeviceInfo {
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
                 bool ta, bool tb, const DeviceInfo& dev, Layout* L);
 
+// One operand of the slice split: op(X) has R rows of K values; `strided` when row r is
+// read along k with stride R (element (r, k) at src[k*R + r]), else src[r*K + k].
+struct SliceDesc {
+    const float* src;
+    int R, K, Rp, Kp;
+    int strided;
+    int vec;            // 16-byte vector loads allowed (alignment and K or R multiple of 4)
+    int nch, kch;       // row-max chunks along K and their length
+    float* pmax;        // [nch][Rp] partial maxima
+    void* out;          // digit panels (or int32 [Rp][Kp] for the reference algorithm)
+    int* expo;          // [Rp] exponents
+    long long max_blocks, split_blocks;
+};
+
+// Fills max_blocks / split_blocks of d.
+void slice_grid(SliceDesc& d);
+
 // Kernel launchers (asynchronous on `stream`).
-void launch_absmax(const float* src, int R, int K, bool strided, int nch, int kch, int Rp,
-                   float* pmax, hipStream_t stream);
-void launch_slice(const float* src, int R, int K, int Rp, int Kp, bool strided, const float* pmax,
-                  int nch, int S, bool int32_out, void* out, int* expo, hipStream_t stream);
+void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream);
+void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream);
 void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
                           const int* eb, float* C, int64_t* partial, hipStream_t stream);
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,

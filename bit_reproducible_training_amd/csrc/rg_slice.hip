@@ -1,22 +1,26 @@
 // Slice-split: FP32 operand -> per-row power-of-two exponent + S int8 digit panels.
 //
 // Replaces quantize_kmajor / quantize_kstrided / emit (repro_gemm_cuda/repro_gemm.cu:36-121).
-// Two bandwidth-bound passes:
-//   absmax_*  partial max|x| of every row of op(X) over a chunk of K (one 64-lane
-//             wavefront per row chunk, or per 64 columns for column access), reduced
-//             across the wavefront with lane shuffles;
-//   slice     one wavefront per (32-row panel, 32-k panel): reduces the partial maxima
-//             of its rows, computes scale_exponent, rounds 16 elements per lane with
-//             fixed_point and writes S int8 digits per element straight into the MFMA
-//             operand panel (1 KiB contiguous per digit and wavefront).
+// Both operands are handled by the same two launches (blocks [0, nA) work on op(A), the
+// rest on op(B)):
+//   absmax_kernel  partial max|x| of every row of op(X) over chunks of K. Row access: one
+//                  64-lane wavefront per (row, chunk), float4 loads, reduced with lane
+//                  shuffles. Column access: a block covers 256 columns (float4 per lane)
+//                  or 64 (scalar), its 4 wavefronts split the chunk's k, reduced in LDS.
+//   split_kernel   a block owns one 32-row panel and 4*G consecutive 32-k panels: it
+//                  reduces the rows' partial maxima once (in LDS), computes scale_exponent,
+//                  and each wavefront rounds 16 elements per lane per panel to the
+//                  fixed-point integer of the definition and writes its S int8 digits
+//                  straight into the MFMA operand panel (1 KiB per digit and wavefront).
 // Max is exact and order-free, so the chunking never changes a bit.
 #include "rg_internal.h"
 #include "repro_gemm_math.h"
 
 namespace rg {
 
-using repro_gemm::fixed_point;
 using repro_gemm::scale_exponent;
+
+constexpr int SPLIT_G = 4;  // k panels per wavefront in split_kernel
 
 __device__ __forceinline__ float wave_max(float m) {
 #pragma unroll
@@ -24,175 +28,318 @@ __device__ __forceinline__ float wave_max(float m) {
     return m;
 }
 
-// Row access: element (r, k) at src[r*K + k]. Wavefront w handles row w / nch, chunk w % nch.
-__global__ void __launch_bounds__(256) absmax_rows(const float* __restrict__ src, int R, int K,
-                                                   int nch, int kch, int Rp,
-                                                   float* __restrict__ pmax) {
-    const int lane = threadIdx.x & 63;
-    const long long w = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (w >= (long long)R * nch) return;
-    const int r = (int)(w / nch), c = (int)(w % nch);
-    const int k0 = c * kch;
-    const int k1 = min(K, k0 + kch);
-    const float* row = src + (size_t)r * K;
-    float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
-    int k = k0 + lane;
-    for (; k + 192 < k1; k += 256) {
-        m0 = fmaxf(m0, fabsf(row[k]));
-        m1 = fmaxf(m1, fabsf(row[k + 64]));
-        m2 = fmaxf(m2, fabsf(row[k + 128]));
-        m3 = fmaxf(m3, fabsf(row[k + 192]));
-    }
-    for (; k < k1; k += 64) m0 = fmaxf(m0, fabsf(row[k]));
-    float m = wave_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-    if (lane == 0) pmax[(size_t)c * Rp + r] = m;
+__device__ __forceinline__ float max4(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
-// Column access: element (r, k) at src[k*R + r]. Wavefront w handles 64 consecutive
-// columns (one per lane) of chunk w % nch.
-__global__ void __launch_bounds__(256) absmax_cols(const float* __restrict__ src, int R, int K,
-                                                   int nch, int kch, int Rp,
-                                                   float* __restrict__ pmax) {
+// Row access, element (r, k) at src[r*K + k]: wavefront w of the operand handles row w / nch,
+// chunk w % nch.
+__device__ void absmax_rows(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63;
-    const long long w = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const long long groups = (R + 63) / 64;
-    if (w >= groups * nch) return;
-    const int g = (int)(w / nch), c = (int)(w % nch);
-    const int r = g * 64 + lane;
-    if (r >= R) return;
-    const int k0 = c * kch;
-    const int k1 = min(K, k0 + kch);
-    const float* col = src + r;
+    const long long w = blk * 4 + (threadIdx.x >> 6);
+    if (w >= (long long)d.R * d.nch) return;
+    const int r = (int)(w / d.nch), c = (int)(w % d.nch);
+    const int k0 = c * d.kch;
+    const int k1 = min(d.K, k0 + d.kch);
+    const float* row = d.src + (size_t)r * d.K;
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
     int k = k0;
-    for (; k + 3 < k1; k += 4) {
-        m0 = fmaxf(m0, fabsf(col[(size_t)k * R]));
-        m1 = fmaxf(m1, fabsf(col[(size_t)(k + 1) * R]));
-        m2 = fmaxf(m2, fabsf(col[(size_t)(k + 2) * R]));
-        m3 = fmaxf(m3, fabsf(col[(size_t)(k + 3) * R]));
+    if (d.vec) {  // K % 4 == 0 and 16-byte aligned rows; kch is a multiple of 4
+        const float4* p = reinterpret_cast<const float4*>(row);
+        int q = k0 / 4 + lane;
+        const int q1 = k1 / 4;
+        for (; q + 192 < q1; q += 256) {
+            m0 = fmaxf(m0, max4(p[q]));
+            m1 = fmaxf(m1, max4(p[q + 64]));
+            m2 = fmaxf(m2, max4(p[q + 128]));
+            m3 = fmaxf(m3, max4(p[q + 192]));
+        }
+        for (; q < q1; q += 64) m0 = fmaxf(m0, max4(p[q]));
+    } else {
+        for (k = k0 + lane; k + 192 < k1; k += 256) {
+            m0 = fmaxf(m0, fabsf(row[k]));
+            m1 = fmaxf(m1, fabsf(row[k + 64]));
+            m2 = fmaxf(m2, fabsf(row[k + 128]));
+            m3 = fmaxf(m3, fabsf(row[k + 192]));
+        }
+        for (; k < k1; k += 64) m0 = fmaxf(m0, fabsf(row[k]));
     }
-    for (; k < k1; ++k) m0 = fmaxf(m0, fabsf(col[(size_t)k * R]));
-    pmax[(size_t)c * Rp + r] = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+    float m = wave_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
+    if (lane == 0) d.pmax[(size_t)c * d.Rp + r] = m;
 }
 
-// Balanced base-128 digits of X, most significant first: X = sum_p d[p] * 128^(S-1-p),
-// |d[0]| <= 127, d[p] in [-64, 63] for p > 0. Exact integer operations only.
-template <int S>
-__device__ __forceinline__ void split_digits(int X, int (&d)[S]) {
-#pragma unroll
-    for (int p = S - 1; p >= 1; --p) {
-        int t = ((X + 64) & 127) - 64;
-        d[p] = t;
-        X = (X - t) >> 7;  // X - t is a multiple of 128
-    }
-    d[0] = X;
-}
-
-// One wavefront per (row panel rp, k panel kp). Lane l owns row rp*32 + l%32 and
-// k = kp*32 + 16*(l/32) + j, j = 0..15.
-template <int S, bool STRIDED, bool INT32_OUT>
-__global__ void __launch_bounds__(256) slice_kernel(const float* __restrict__ src, int R, int K,
-                                                    int Rp, int Kp, const float* __restrict__ pmax,
-                                                    int nch, void* __restrict__ out,
-                                                    int* __restrict__ expo, int vec_ok) {
-    const int lane = threadIdx.x & 63;
-    const int npk = Kp / PANEL_K;
-    const long long w = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (w >= (long long)(Rp / PANEL_ROWS) * npk) return;
-    const int rp = (int)(w / npk), kp = (int)(w % npk);
-    const int r = rp * PANEL_ROWS + (lane & 31);
-    const int h = lane >> 5;
-
-    float m = 0.0f;
-    if (r < R)
-        for (int c = 0; c < nch; ++c) m = fmaxf(m, pmax[(size_t)c * Rp + r]);
-    const int se = scale_exponent(m);
-    if (kp == 0 && h == 0) expo[r] = se;
-
-    const int k0 = kp * PANEL_K + 16 * h;
-    float x[16];
-    if (r < R) {
-        if (STRIDED) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                x[j] = (k0 + j < K) ? src[(size_t)(k0 + j) * R + r] : 0.0f;
-        } else if (vec_ok && k0 + 16 <= K) {
-            const float4* p = reinterpret_cast<const float4*>(src + (size_t)r * K + k0);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float4 v = p[q];
-                x[4 * q + 0] = v.x;
-                x[4 * q + 1] = v.y;
-                x[4 * q + 2] = v.z;
-                x[4 * q + 3] = v.w;
+// Column access, element (r, k) at src[k*R + r]: block g covers cols columns of chunk c;
+// its 4 wavefronts take every 4th k of the chunk and combine in LDS.
+__device__ void absmax_cols(const SliceDesc& d, long long blk) {
+    __shared__ float4 part[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int cols = d.vec ? 256 : 64;
+    const long long groups = (d.R + cols - 1) / cols;
+    if (blk >= groups * d.nch) return;
+    const int g = (int)(blk / d.nch), c = (int)(blk % d.nch);
+    const int k0 = c * d.kch;
+    const int k1 = min(d.K, k0 + d.kch);
+    float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (d.vec) {  // R % 4 == 0 and 16-byte aligned: lane owns columns 4*lane .. 4*lane+3
+        const int r = g * 256 + 4 * lane;
+        if (r < d.R) {
+            const float* base = d.src + r;
+            int k = k0 + wv;
+            for (; k + 12 < k1; k += 16) {
+                float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.R);
+                float4 b = *reinterpret_cast<const float4*>(base + (size_t)(k + 4) * d.R);
+                float4 e = *reinterpret_cast<const float4*>(base + (size_t)(k + 8) * d.R);
+                float4 f = *reinterpret_cast<const float4*>(base + (size_t)(k + 12) * d.R);
+                m.x = fmaxf(m.x, fmaxf(fmaxf(fabsf(a.x), fabsf(b.x)), fmaxf(fabsf(e.x), fabsf(f.x))));
+                m.y = fmaxf(m.y, fmaxf(fmaxf(fabsf(a.y), fabsf(b.y)), fmaxf(fabsf(e.y), fabsf(f.y))));
+                m.z = fmaxf(m.z, fmaxf(fmaxf(fabsf(a.z), fabsf(b.z)), fmaxf(fabsf(e.z), fabsf(f.z))));
+                m.w = fmaxf(m.w, fmaxf(fmaxf(fabsf(a.w), fabsf(b.w)), fmaxf(fabsf(e.w), fabsf(f.w))));
             }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) x[j] = (k0 + j < K) ? src[(size_t)r * K + k0 + j] : 0.0f;
+            for (; k < k1; k += 4) {
+                float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.R);
+                m.x = fmaxf(m.x, fabsf(a.x));
+                m.y = fmaxf(m.y, fabsf(a.y));
+                m.z = fmaxf(m.z, fabsf(a.z));
+                m.w = fmaxf(m.w, fabsf(a.w));
+            }
         }
     } else {
+        const int r = g * 64 + lane;
+        if (r < d.R) {
+            const float* base = d.src + r;
+            int k = k0 + wv;
+            for (; k + 12 < k1; k += 16) {
+                m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.R]));
+                m.y = fmaxf(m.y, fabsf(base[(size_t)(k + 4) * d.R]));
+                m.z = fmaxf(m.z, fabsf(base[(size_t)(k + 8) * d.R]));
+                m.w = fmaxf(m.w, fabsf(base[(size_t)(k + 12) * d.R]));
+            }
+            for (; k < k1; k += 4) m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.R]));
+            m.x = fmaxf(fmaxf(m.x, m.y), fmaxf(m.z, m.w));
+        }
+    }
+    part[wv][lane] = m;
+    __syncthreads();
+    if (wv == 0) {
+        float4 t = part[0][lane];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            float4 u = part[i][lane];
+            t.x = fmaxf(t.x, u.x);
+            t.y = fmaxf(t.y, u.y);
+            t.z = fmaxf(t.z, u.z);
+            t.w = fmaxf(t.w, u.w);
+        }
+        float* out = d.pmax + (size_t)c * d.Rp;
+        if (d.vec) {
+            const int r = g * 256 + 4 * lane;
+            if (r < d.R) *reinterpret_cast<float4*>(out + r) = t;  // Rp % 32 == 0: in range
+        } else {
+            const int r = g * 64 + lane;
+            if (r < d.R) out[r] = t.x;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) absmax_kernel(SliceDesc a, SliceDesc b) {
+    const long long blk = blockIdx.x;
+    if (blk < a.max_blocks) {
+        if (a.strided) absmax_cols(a, blk); else absmax_rows(a, blk);
+    } else {
+        if (b.strided) absmax_cols(b, blk - a.max_blocks); else absmax_rows(b, blk - a.max_blocks);
+    }
+}
+
+// Per-row constants of the rounding X = RNE(x * 2^(7(S-1) - se)), clamped to +-lim.
+// The scale is applied as two multiplications by normal powers of two, as the definition
+// does (repro_gemm_math.cuh:44-55, 71-83): with n = 7(S-1) - se in [-122, 163], both
+// factors are normal; the product is exact unless it is subnormal, and then |v| < 2^-126
+// rounds to 0 whatever the intermediate rounding was. Needs IEEE f32 denormals, which the
+// gfx950 kernels of this library run with (denorm mode 3, no flushing).
+struct RowScale {
+    float p1, p2;
+    int lim;
+};
+
+template <int S>
+__device__ __forceinline__ RowScale row_scale(int se) {
+    const int n = 7 * (S - 1) - se;
+    const int n1 = n >> 1, n2 = n - n1;
+    RowScale rs;
+    rs.p1 = __uint_as_float((uint32_t)(n1 + 127) << 23);
+    rs.p2 = __uint_as_float((uint32_t)(n2 + 127) << 23);
+    rs.lim = 127 << (7 * (S - 1));
+    return rs;
+}
+
+__device__ __forceinline__ int round_fixed(float x, const RowScale& rs) {
+    const float v = (x * rs.p1) * rs.p2;
+    const int X = (int)__builtin_rintf(v);  // v_rndne_f32: nearest-even; |v| < 2^22 here
+    return min(max(X, -rs.lim), rs.lim);
+}
+
+// Four bytes (low byte of each argument) packed little-endian with v_perm_b32.
+__device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b1, (uint32_t)b0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)b3, (uint32_t)b2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// Rounds 16 values and writes them: S digit planes of 16 bytes (balanced base 128, most
+// significant first: X = sum_p d_p 128^(S-1-p), |d_0| <= 127, d_p in [-64, 63] for p > 0),
+// or 16 int32 fixed-point values for INT32_OUT.
+template <int S, bool INT32_OUT>
+__device__ __forceinline__ void emit_panel(const SliceDesc& d, const float (&x)[16], const RowScale& rs,
+                                           int rp, int kp, int r, int h, int lane) {
+    int X[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) X[j] = round_fixed(x[j], rs);
+    if (INT32_OUT) {
+        int4* o = reinterpret_cast<int4*>(static_cast<int32_t*>(d.out) + (size_t)r * d.Kp + kp * PANEL_K + 16 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = make_int4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
+        return;
+    }
+    int dg[S][16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        int v = X[j];
+#pragma unroll
+        for (int p = S - 1; p >= 1; --p) {
+            dg[p][j] = (v << 25) >> 25;  // v_bfe_i32: the digit in [-64, 63] congruent to v mod 128
+            v = (v + 64) >> 7;           // == (v - digit) / 128 exactly
+        }
+        dg[0][j] = v;
+    }
+    const int npk = d.Kp / PANEL_K;
+    uint4* o = reinterpret_cast<uint4*>(d.out) + ((size_t)rp * npk + kp) * S * (PANEL_BYTES / 16) + lane;
+#pragma unroll
+    for (int p = 0; p < S; ++p)
+        o[(size_t)p * (PANEL_BYTES / 16)] =
+            make_uint4(pack4(dg[p][0], dg[p][1], dg[p][2], dg[p][3]), pack4(dg[p][4], dg[p][5], dg[p][6], dg[p][7]),
+                       pack4(dg[p][8], dg[p][9], dg[p][10], dg[p][11]), pack4(dg[p][12], dg[p][13], dg[p][14], dg[p][15]));
+}
+
+// The 16 values of lane (row r, half h) in panel kp; zero outside the matrix.
+__device__ __forceinline__ void load_panel(const SliceDesc& d, int kp, int r, int h, bool checked,
+                                           float (&x)[16]) {
+    const int k0 = kp * PANEL_K + 16 * h;
+    if (r >= d.R) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) x[j] = 0.0f;
+        return;
     }
-
-    if (INT32_OUT) {
-        int4* o = reinterpret_cast<int4*>(static_cast<int32_t*>(out) + (size_t)r * Kp + k0);
+    if (d.strided) {
+        const float* p = d.src + (size_t)k0 * d.R + r;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            o[q] = make_int4(fixed_point(x[4 * q], se, S), fixed_point(x[4 * q + 1], se, S),
-                             fixed_point(x[4 * q + 2], se, S), fixed_point(x[4 * q + 3], se, S));
-    } else {
-        uint32_t word[S][4];
+        for (int j = 0; j < 16; ++j) x[j] = (!checked || k0 + j < d.K) ? p[(size_t)j * d.R] : 0.0f;
+    } else if (d.vec && (!checked || k0 + 16 <= d.K)) {
+        const float4* p = reinterpret_cast<const float4*>(d.src + (size_t)r * d.K + k0);
 #pragma unroll
-        for (int p = 0; p < S; ++p)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) word[p][q] = 0;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            int d[S];
-            split_digits<S>(fixed_point(x[j], se, S), d);
-#pragma unroll
-            for (int p = 0; p < S; ++p) word[p][j >> 2] |= ((uint32_t)d[p] & 0xFFu) << (8 * (j & 3));
+        for (int q = 0; q < 4; ++q) {
+            float4 v = p[q];
+            x[4 * q + 0] = v.x;
+            x[4 * q + 1] = v.y;
+            x[4 * q + 2] = v.z;
+            x[4 * q + 3] = v.w;
         }
-        uint4* o = reinterpret_cast<uint4*>(static_cast<int8_t*>(out)) +
-                   ((size_t)(rp * npk + kp) * S) * (PANEL_BYTES / 16) + lane;
+    } else {
+        const float* p = d.src + (size_t)r * d.K + k0;
 #pragma unroll
-        for (int p = 0; p < S; ++p)
-            o[(size_t)p * (PANEL_BYTES / 16)] = make_uint4(word[p][0], word[p][1], word[p][2], word[p][3]);
+        for (int j = 0; j < 16; ++j) x[j] = (!checked || k0 + j < d.K) ? p[j] : 0.0f;
     }
 }
 
-void launch_absmax(const float* src, int R, int K, bool strided, int nch, int kch, int Rp,
-                   float* pmax, hipStream_t stream) {
-    long long waves = strided ? (long long)((R + 63) / 64) * nch : (long long)R * nch;
-    unsigned blocks = (unsigned)((waves + 3) / 4);
-    if (strided)
-        absmax_cols<<<blocks, 256, 0, stream>>>(src, R, K, nch, kch, Rp, pmax);
-    else
-        absmax_rows<<<blocks, 256, 0, stream>>>(src, R, K, nch, kch, Rp, pmax);
+template <int S, bool INT32_OUT>
+__device__ void split_operand(const SliceDesc& d, long long blk) {
+    __shared__ float smax[8][32];
+    __shared__ int sse[32];
+    const int npk = d.Kp / PANEL_K;
+    const int rpanels = d.Rp / PANEL_ROWS;
+    const int kgroups = (npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G);
+    // Column access: neighbouring blocks take neighbouring row panels of the same k rows;
+    // row access: neighbouring blocks continue along k of the same rows.
+    int rp, kg;
+    if (d.strided) {
+        rp = (int)(blk % rpanels);
+        kg = (int)(blk / rpanels);
+    } else {
+        rp = (int)(blk / kgroups);
+        kg = (int)(blk % kgroups);
+    }
+    const int t = threadIdx.x;
+    {   // row maxima of this panel's 32 rows, reduced once for the whole block
+        const int rr = t & 31, c0 = t >> 5;
+        const int row = rp * PANEL_ROWS + rr;
+        float m = 0.0f;
+        if (row < d.R)
+            for (int c = c0; c < d.nch; c += 8) m = fmaxf(m, d.pmax[(size_t)c * d.Rp + row]);
+        smax[c0][rr] = m;
+    }
+    __syncthreads();
+    if (t < 32) {
+        float m = smax[0][t];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) m = fmaxf(m, smax[i][t]);
+        const int se = scale_exponent(m);  // rows >= R have m == 0, so se == 0
+        sse[t] = se;
+        if (kg == 0) d.expo[rp * PANEL_ROWS + t] = se;
+    }
+    __syncthreads();
+    const int lane = t & 63, wv = t >> 6;
+    const int r = rp * PANEL_ROWS + (lane & 31), h = lane >> 5;
+    const RowScale rs = row_scale<S>(sse[lane & 31]);
+    const int kpb = kg * 4 * SPLIT_G + wv * SPLIT_G;
+    if (kpb + SPLIT_G <= npk && (kpb + SPLIT_G) * PANEL_K <= d.K) {
+        // Every panel of this wavefront lies inside K: issue all loads, then round.
+        float x[SPLIT_G][16];
+#pragma unroll
+        for (int g = 0; g < SPLIT_G; ++g) load_panel(d, kpb + g, r, h, false, x[g]);
+#pragma unroll
+        for (int g = 0; g < SPLIT_G; ++g) emit_panel<S, INT32_OUT>(d, x[g], rs, rp, kpb + g, r, h, lane);
+    } else {
+        for (int g = 0; g < SPLIT_G; ++g) {
+            const int kp = kpb + g;
+            if (kp >= npk) break;
+            float x[16];
+            load_panel(d, kp, r, h, true, x);
+            emit_panel<S, INT32_OUT>(d, x, rs, rp, kp, r, h, lane);
+        }
+    }
 }
 
-template <int S, bool I32>
-static void launch_slice_s(const float* src, int R, int K, int Rp, int Kp, bool strided,
-                           const float* pmax, int nch, void* out, int* expo, hipStream_t stream) {
-    long long waves = (long long)(Rp / PANEL_ROWS) * (Kp / PANEL_K);
-    unsigned blocks = (unsigned)((waves + 3) / 4);
-    int vec_ok = (K % 4 == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
-    if (strided)
-        slice_kernel<S, true, I32><<<blocks, 256, 0, stream>>>(src, R, K, Rp, Kp, pmax, nch, out, expo, vec_ok);
-    else
-        slice_kernel<S, false, I32><<<blocks, 256, 0, stream>>>(src, R, K, Rp, Kp, pmax, nch, out, expo, vec_ok);
+template <int S, bool INT32_OUT>
+__global__ void __launch_bounds__(256) split_kernel(SliceDesc a, SliceDesc b) {
+    const long long blk = blockIdx.x;
+    if (blk < a.split_blocks) split_operand<S, INT32_OUT>(a, blk);
+    else split_operand<S, INT32_OUT>(b, blk - a.split_blocks);
 }
 
-void launch_slice(const float* src, int R, int K, int Rp, int Kp, bool strided, const float* pmax,
-                  int nch, int S, bool int32_out, void* out, int* expo, hipStream_t stream) {
+// Grid sizes of the two passes for one operand.
+void slice_grid(SliceDesc& d) {
+    if (d.strided) {
+        const int cols = d.vec ? 256 : 64;
+        d.max_blocks = (long long)((d.R + cols - 1) / cols) * d.nch;
+    } else {
+        d.max_blocks = ((long long)d.R * d.nch + 3) / 4;
+    }
+    const int npk = d.Kp / PANEL_K;
+    d.split_blocks = (long long)(d.Rp / PANEL_ROWS) * ((npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G));
+}
+
+void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream) {
+    absmax_kernel<<<(unsigned)(a.max_blocks + b.max_blocks), 256, 0, stream>>>(a, b);
+}
+
+void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream) {
+    const unsigned blocks = (unsigned)(a.split_blocks + b.split_blocks);
     switch (S * 2 + (int32_out ? 1 : 0)) {
-        case 2: launch_slice_s<1, false>(src, R, K, Rp, Kp, strided, pmax, nch, out, expo, stream); break;
-        case 3: launch_slice_s<1, true>(src, R, K, Rp, Kp, strided, pmax, nch, out, expo, stream); break;
-        case 4: launch_slice_s<2, false>(src, R, K, Rp, Kp, strided, pmax, nch, out, expo, stream); break;
-        case 5: launch_slice_s<2, true>(src, R, K, Rp, Kp, strided, pmax, nch, out, expo, stream); break;
-        case 6: launch_slice_s<3, false>(src, R, K, Rp, Kp, strided, pmax, nch, out, expo, stream); break;
-        case 7: launch_slice_s<3, true>(src, R, K, Rp, Kp, strided, pmax, nch, out, expo, stream); break;
+        case 2: split_kernel<1, false><<<blocks, 256, 0, stream>>>(a, b); break;
+        case 3: split_kernel<1, true><<<blocks, 256, 0, stream>>>(a, b); break;
+        case 4: split_kernel<2, false><<<blocks, 256, 0, stream>>>(a, b); break;
+        case 5: split_kernel<2, true><<<blocks, 256, 0, stream>>>(a, b); break;
+        case 6: split_kernel<3, false><<<blocks, 256, 0, stream>>>(a, b); break;
+        case 7: split_kernel<3, true><<<blocks, 256, 0, stream>>>(a, b); break;
         default: break;
     }
 }
