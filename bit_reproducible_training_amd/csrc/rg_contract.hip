@@ -3,12 +3,13 @@
 // Replaces gemm_wmma_i8 / gemm_tiled_dp4a / gemm_reference / reduce_round / write_output
 // (repro_gemm_cuda/repro_gemm.cu:124-165, 189-364).
 //
-// contract_mfma: a 256-thread block (4 wavefronts in 2x2) owns a (64*TI) x (64*TJ) tile of
-// C; each wavefront owns TI x TJ tiles of 32x32 and runs V_MFMA_I32_32X32X32_I8 on them.
+// contract_mfma: a block of WGM x WGN wavefronts owns a (32*WGM*WTI) x (32*WGN*WTJ) tile of
+// C; each wavefront owns WTI x WTJ tiles of 32x32 and runs V_MFMA_I32_32X32X32_I8 on them.
 // Digit pairs (p, q) with the same level p + q share one int32 accumulator per output,
-// so a wavefront holds (2S-1) * TI * TJ accumulator tiles. Each pipeline stage copies the
-// block's digit panels for 64 values of k from HBM into LDS (double-buffered); operand
-// fragments are then read from LDS with one 16-byte read per lane and panel. All level
+// so a wavefront holds (2S-1) * WTI * WTJ accumulator tiles. Each pipeline stage brings
+// the block's digit panels for 64 values of k from HBM into a three-slot LDS ring with
+// direct global->LDS loads issued two stages ahead; operand fragments are read from LDS
+// with one 16-byte read per lane and panel. All level
 // accumulators of one output sit in the same lane and register index, so the epilogue
 // combines them in int64 without any data exchange:
 //     T = sum_L acc_L * 2^(7 (2S-2-L)) = sum_k X[r,k] * Y[c,k]   (exact)
@@ -25,11 +26,16 @@ using repro_gemm::round_to_float;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// s_waitcnt on vector-memory operations only: wait until at most n are outstanding.
+#define RG_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define RG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
 template <int S, int WTI, int WTJ, int WGM, int WGN>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
               const int* __restrict__ eA, const int* __restrict__ eB, float* __restrict__ C,
               int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)  // buffer resources exist only in the device pass
     constexpr int L = 2 * S - 1;
     constexpr int NW = WGM * WGN;                  // wavefronts per block
     constexpr int BM = WGM * WTI * 32, BN = WGN * WTJ * 32;
@@ -38,7 +44,10 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     constexpr int PT = PA + PB;
     constexpr int PW = PT / NW;                    // panels copied per wavefront per stage
     static_assert(PT % NW == 0, "stage panels must split evenly over the wavefronts");
-    __shared__ v4i lds[2][PT][64];
+    static_assert(PW < 64, "vmcnt immediate");
+    // Three-stage ring, filled by direct global->LDS loads (buffer_load_dwordx4 ... lds: lane
+    // i's 16 bytes land at the wavefront-uniform LDS base + 16 i, which is the panel layout).
+    __shared__ v4i lds[3][PT][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -49,25 +58,30 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     const int s0 = (int)((long long)nsteps * part / split);
     const int s1 = (int)((long long)nsteps * (part + 1) / split);
     const size_t row_stride = (size_t)(Kp / PANEL_K) * S * (PANEL_BYTES / 16);  // in v4i
-    const size_t step_stride = (size_t)2 * S * (PANEL_BYTES / 16);              // in v4i
 
-    // Source of each panel this wavefront copies, at step 0 (wavefront-uniform offsets).
-    size_t soff[PW];
-    const v4i* sbase[PW];
+    // One buffer resource per panel this wavefront copies: base = the panel at stage s0,
+    // range = this part's stages, so every offset is 32-bit whatever K is and an offset out
+    // of range would read zeros instead of faulting. Everything here is wavefront-uniform
+    // (scalar registers); the only per-lane operand of the copies is lane * 16.
+    const uint32_t step_bytes = 2u * S * PANEL_BYTES;
+    const uint32_t part_bytes = (uint32_t)(s1 - s0) * step_bytes;
+    __amdgpu_buffer_rsrc_t rsrc[PW];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
         const int pi = wave + NW * i;
+        const int8_t* base;
         if (pi < PA) {
             const int rl = pi / (2 * S), o = pi % (2 * S);
-            sbase[i] = reinterpret_cast<const v4i*>(QA);
-            soff[i] = (size_t)(tm * (BM / PANEL_ROWS) + rl) * row_stride + (size_t)o * (PANEL_BYTES / 16);
+            base = QA + ((size_t)(tm * (BM / PANEL_ROWS) + rl) * row_stride + (size_t)o * (PANEL_BYTES / 16)) * 16;
         } else {
             const int pb = pi - PA;
             const int cl = pb / (2 * S), o = pb % (2 * S);
-            sbase[i] = reinterpret_cast<const v4i*>(QB);
-            soff[i] = (size_t)(tn * (BN / PANEL_ROWS) + cl) * row_stride + (size_t)o * (PANEL_BYTES / 16);
+            base = QB + ((size_t)(tn * (BN / PANEL_ROWS) + cl) * row_stride + (size_t)o * (PANEL_BYTES / 16)) * 16;
         }
+        base += (size_t)s0 * step_bytes;
+        rsrc[i] = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)part_bytes, 0x00020000);
     }
+    const uint32_t voff = (uint32_t)lane * 16u;
 
     v16i acc[L][WTI][WTJ];
 #pragma unroll
@@ -79,32 +93,23 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[l][ti][tj][e] = 0;
 
-    v4i stage[PW];
-    if (s0 < s1) {
+    auto issue = [&](v4i (*slot)[64], int step) {
+        const uint32_t soff = (uint32_t)(step - s0) * step_bytes;
 #pragma unroll
-        for (int i = 0; i < PW; ++i) stage[i] = sbase[i][soff[i] + (size_t)s0 * step_stride + lane];
-#pragma unroll
-        for (int i = 0; i < PW; ++i) lds[0][wave + NW * i][lane] = stage[i];
-    }
-    __syncthreads();
-
-    for (int s = s0; s < s1; ++s) {
-        const int cur = (s - s0) & 1;
-        const bool more = s + 1 < s1;
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < PW; ++i)
-                stage[i] = sbase[i][soff[i] + (size_t)(s + 1) * step_stride + lane];
-        }
+        for (int i = 0; i < PW; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[i], RG_LDS_PTR(&slot[wave + NW * i][0]), 16, voff,
+                                                     soff, 0, 0);
+    };
+    auto compute = [&](v4i (*slot)[64]) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             v4i a[S][WTI], b[S][WTJ];
 #pragma unroll
             for (int p = 0; p < S; ++p) {
 #pragma unroll
-                for (int ti = 0; ti < WTI; ++ti) a[p][ti] = lds[cur][((wm * WTI + ti) * 2 + kk) * S + p][lane];
+                for (int ti = 0; ti < WTI; ++ti) a[p][ti] = slot[((wm * WTI + ti) * 2 + kk) * S + p][lane];
 #pragma unroll
-                for (int tj = 0; tj < WTJ; ++tj) b[p][tj] = lds[cur][PA + ((wn * WTJ + tj) * 2 + kk) * S + p][lane];
+                for (int tj = 0; tj < WTJ; ++tj) b[p][tj] = slot[PA + ((wn * WTJ + tj) * 2 + kk) * S + p][lane];
             }
 #pragma unroll
             for (int p = 0; p < S; ++p)
@@ -116,12 +121,33 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
                         for (int tj = 0; tj < WTJ; ++tj)
                             acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
                                 a[p][ti], b[q][tj], acc[p + q][ti][tj], 0, 0, 0);
+            // Operands of the second sub-step are read after the first's MFMAs are issued,
+            // which bounds the live operand registers to one sub-step.
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < PW; ++i) lds[cur ^ 1][wave + NW * i][lane] = stage[i];
-        }
-        __syncthreads();
+    };
+    // Stage s: wait for this wavefront's loads of stage s (stage s+1's may stay in flight),
+    // barrier (everyone's stage s has landed and everyone has finished stage s-1, whose slot
+    // is refilled next), issue stage s+2, contract stage s. Every LDS read of a stage feeds
+    // an MFMA issued before the next barrier, so no read can see the refill.
+    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s) {
+        if (s + 1 < s1) RG_WAIT_VMCNT(PW);
+        else RG_WAIT_VMCNT(0);
+        // The hardware barrier, plus a compiler barrier for LDS accesses (the s_barrier
+        // intrinsic alone does not keep memory operations from moving across it, and
+        // __syncthreads() would also wait for the loads still in flight into other slots).
+        asm volatile("s_barrier" ::: "memory");
+        if (s + 2 < s1) issue(refill, s + 2);
+        compute(cur);
+    };
+
+    if (s0 < s1) issue(lds[0], s0);
+    if (s0 + 1 < s1) issue(lds[1], s0 + 1);
+    int cur = 0;
+    for (int s = s0; s < s1; ++s) {
+        const int refill = cur == 0 ? 2 : cur - 1;  // slot of stage s - 1 == slot of stage s + 2
+        stage(lds[cur], lds[refill], s);
+        cur = cur == 2 ? 0 : cur + 1;
     }
 
     // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
@@ -153,6 +179,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+#endif
 }
 
 // The definition, as plainly as possible: one thread per output, int64 sum of X * Y over
