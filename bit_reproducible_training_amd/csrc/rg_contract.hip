@@ -121,9 +121,6 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
                         for (int tj = 0; tj < WTJ; ++tj)
                             acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
                                 a[p][ti], b[q][tj], acc[p + q][ti][tj], 0, 0, 0);
-            // Operands of the second sub-step are read after the first's MFMAs are issued,
-            // which bounds the live operand registers to one sub-step.
-            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // Stage s: wait for this wavefront's loads of stage s (stage s+1's may stay in flight),

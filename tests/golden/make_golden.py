@@ -20,10 +20,31 @@ from golden import configs  # noqa: E402
 from oracle import oracle as O  # noqa: E402
 
 OUT = os.path.join(HERE, "baseline_configs.json")
+BENCH_OUT = os.path.join(HERE, "bench_fixtures.json")
 REF_CHECK_MAX_MACS = 2e10
 
 
+def bench_main():
+    """Fixture of bench.py's headline inputs: 4096^3, S=3, A then B N(0,1) from one stream
+    seeded 12345 (the reference bench's recipe, repro_gemm_cuda/bench_repro_gemm.cu:47-49)."""
+    n = 4096
+    A = O.gen_normal(n * n, 1.0, 12345, 0)
+    B = O.gen_normal(n * n, 1.0, 12345, n * n)
+    C = O.cpu_gemm(A, B, n, n, n, 0, 0, 3)
+    row = dict(name="bench.4096cube.normal", M=n, N=n, K=n, ta=0, tb=0, S=3,
+               in_hash="%016x" % O.fnv_chain(A, B), out_hash="%016x" % O.fnv1a64(C))
+    if O.ref is not None:
+        R = O.ref_cpu_gemm(A, B, n, n, n, 0, 0, 3)
+        assert O.fnv1a64(R) == O.fnv1a64(C), "oracle and reference CPU path disagree"
+        row["ref_checked"] = True
+    with open(BENCH_OUT, "w") as f:
+        json.dump({"generator": "tests/golden/make_golden.py --bench", "cases": [row]}, f, indent=1)
+    print(row)
+
+
 def main():
+    if "--bench" in sys.argv:
+        return bench_main()
     rows = []
     for case in configs.all_cases():
         t0 = time.time()

@@ -11,3 +11,13 @@ def test_bench_adversarial_inputs_match_recipe():
         got = bench._adversarial(rows, cols, seed, pr, neg)
         want = O.gen_adversarial(rows, cols, seed, pr, neg)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_bench_normal_inputs_match_oracle_stream():
+    n = 64
+    A, B = bench.make_normal(n)
+    assert np.array_equal(A.reshape(-1).view(np.uint32), O.gen_normal(n * n, 1.0, 12345, 0).view(np.uint32))
+    assert np.array_equal(B.reshape(-1).view(np.uint32), O.gen_normal(n * n, 1.0, 12345, n * n).view(np.uint32))
+    # chunk boundaries of the threaded generator do not change bits
+    x = bench.normal_stream(5000, 7, 3, chunk=1000)
+    assert np.array_equal(x.view(np.uint32), O.gen_normal(5000, 1.0, 7, 3).view(np.uint32))
