@@ -88,7 +88,7 @@ def make_adversarial(n):
     return np.ascontiguousarray(A), np.ascontiguousarray(B)
 
 
-def _normal_chunk(out, a, b, seed, first):
+def _normal_chunk(out, a, b, seed, first, scale=1.0):
     """Elements [a, b): Irwin-Hall sum of 12 draws (element i uses draws 12 i .. 12 i + 11),
     summed in the same order as the reference's Rng::normal (repro_test_util.h:41)."""
     j = np.arange(12, dtype=np.uint64)
@@ -97,15 +97,15 @@ def _normal_chunk(out, a, b, seed, first):
     t = np.zeros(b - a)
     for k in range(12):
         t += u[:, k]
-    out[a:b] = (t - 6.0).astype(np.float32)
+    out[a:b] = (scale * (t - 6.0)).astype(np.float32)
 
 
-def normal_stream(n, seed, first=0, chunk=1 << 20):
+def normal_stream(n, seed, first=0, chunk=1 << 20, scale=1.0):
     from concurrent.futures import ThreadPoolExecutor
 
     out = np.empty(n, np.float32)
     with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
-        list(ex.map(lambda a: _normal_chunk(out, a, min(n, a + chunk), seed, first),
+        list(ex.map(lambda a: _normal_chunk(out, a, min(n, a + chunk), seed, first, scale),
                     range(0, n, chunk)))
     return out
 
@@ -209,6 +209,70 @@ def time_workload(torch, rg, A, B, n, steps, warmup, calibrate=False):
     return out
 
 
+def suite(torch, rg, reps=10, warmup=2):
+    """The 21 GEMMs of the reference's GPT-2 operation suite at 1024 tokens, S=3, with its
+    input recipe (gpt2_ops_suite.cu:193-233, 463-483) and its timing method (median of `reps`
+    event-timed calls after `warmup`, gpt2_ops_suite.cu:622-640), next to the times it recorded
+    on three NVIDIA GPUs and an FP32 torch.matmul baseline on this GPU (not reproducible).
+    Output bits of these ops are checked against the recorded hashes by
+    tests/test_gpu_parity.py::test_reference_suite_hashes_gpu."""
+    with open(os.path.join(REPO, "tests", "golden", "suite_gemm_s3.json")) as f:
+        ops = json.load(f)["gemm"]
+    torch.backends.cuda.matmul.allow_tf32 = False
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    rows = []
+    for op in ops:
+        M, N, K, ta, tb = op["M"], op["N"], op["K"], op["ta"], op["tb"]
+        A = torch.from_numpy(normal_stream(M * K, op["seed"], scale=op["sa"])).cuda()
+        B = torch.from_numpy(normal_stream(K * N, op["seed"] + 1, scale=op["sb"])).cuda()
+        C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        cfg = rg.Config(slices=3, trans_a=ta, trans_b=tb)
+        plan = rg.make_plan(M, N, K, cfg)
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+        sp = torch.cuda.current_stream().cuda_stream
+
+        def run():
+            code = rg.repro_gemm_fp32_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, cfg,
+                                         ws.data_ptr(), ws.numel(), sp)
+            if code != 0:
+                raise rg.ReproGemmError(code, op["name"])
+
+        opA = A.view(K, M).t() if ta else A.view(M, K)
+        opB = B.view(N, K).t() if tb else B.view(K, N)
+
+        def base():
+            torch.matmul(opA, opB)
+
+        def timed(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t = []
+            for _ in range(reps):
+                e0.record()
+                fn()
+                e1.record()
+                e1.synchronize()
+                t.append(e0.elapsed_time(e1))
+            return statistics.median(t)
+
+        ms, base_ms = timed(run), timed(base)
+        ref = op.get("reference_gpu_ms", {})
+        best_ref = min((v["ms"] for v in ref.values()), default=None)
+        rows.append({"op": op["name"], "shape": op["shape"], "ms": round(ms, 4),
+                     "tflops": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2),
+                     "torch_fp32_ms": round(base_ms, 4),
+                     "plan": "%dx%d split %d" % (plan.tile_m, plan.tile_n, plan.split_k),
+                     "reference_best_gpu_ms": best_ref,
+                     "speedup_vs_reference_best": round(best_ref / ms, 1) if best_ref else None})
+        del A, B, C, ws
+    total = sum(r["ms"] for r in rows)
+    ref_total = sum(r["reference_best_gpu_ms"] for r in rows if r["reference_best_gpu_ms"])
+    print(json.dumps({"mode": "suite", "tokens": 1024, "slices": 3, "ops": rows,
+                      "total_ms": round(total, 3), "reference_best_gpu_total_ms": round(ref_total, 3)}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +283,8 @@ def main():
     ap.add_argument("--no-adversarial", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--suite", action="store_true",
+                    help="time the reference GPT-2 suite's 21 GEMMs (1024 tokens) instead")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 device-to-device copies of 256 MiB (a plain copy kernel of "
                          "known size, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -232,6 +298,10 @@ def main():
     import torch
 
     import bit_reproducible_training_amd as rg
+
+    if args.suite:
+        suite(torch, rg)
+        return
 
     n = args.size
     S = 3
@@ -255,6 +325,11 @@ def main():
         cpu, checks, _ = cpu_baseline(A, B, n, head["C"], args.cpu_threads, args.cpu_reps, fixtures,
                                       adv["C"] if adv else None)
     bit_exact = all(checks.values()) if checks else None
+
+    # The practical ceiling: sustained int8 MFMA rate with register operands (no memory),
+    # dense random bytes and zeros; the matrix cores' power draw depends on the operands.
+    ceiling = {"dense_tops": round(rg.measure_mfma_int8_rate(True), 1),
+               "zero_tops": round(rg.measure_mfma_int8_rate(False), 1)}
 
     M = N = K = n
     ms = head["ms_per_step"]
@@ -286,6 +361,8 @@ def main():
                      "traffic": TRAFFIC_BYTES,
                      "kernel": "contract_mfma<3,2,1,2,4>: int8 ops = 9 * 2MNK per launch, one "
                                "launch per step; achieved = ops / HIP-event duration"},
+        "mfma_ceiling_measured": dict(ceiling, contract_frac_of_dense=round(
+            contract_tops / ceiling["dense_tops"], 4) if ceiling["dense_tops"] else None),
         "cpu_baseline": cpu,
         "bit_exact": bit_exact,
         "checks": checks,

@@ -13,6 +13,7 @@ from .repro_gemm import (  # noqa: F401
     algo_name,
     gemm,
     make_plan,
+    measure_mfma_int8_rate,
     plan_for_device,
     repro_gemm_fp32,
     repro_gemm_fp32_ws,

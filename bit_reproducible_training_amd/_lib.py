@@ -70,6 +70,7 @@ _SIGNATURES = {
     "rg_workspace_layout": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                            ctypes.POINTER(rg_config),
                                            ctypes.POINTER(rg_layout_info)]),
+    "rg_measure_mfma_int8_rate": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "rg_plan_for_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),

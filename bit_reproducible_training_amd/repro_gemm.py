@@ -114,6 +114,14 @@ def repro_gemm_fp32(A, B, C, M, N, K, cfg=None, stream=None):
     return lib.rg_gemm_fp32(A, B, C, int(M), int(N), int(K), ctypes.byref(c), stream)
 
 
+def measure_mfma_int8_rate(dense=True):
+    """Sustained int8 MFMA TOP/s of the current device with register operands (dense random
+    bytes or zeros); the practical ceiling of the contraction under the power limit."""
+    out = ctypes.c_double()
+    _check(lib.rg_measure_mfma_int8_rate(int(bool(dense)), ctypes.byref(out)), "measure_mfma_int8_rate")
+    return out.value
+
+
 def algo_name(a):
     return lib.rg_algo_name(int(a)).decode()
 

@@ -115,6 +115,13 @@ int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_inf
 int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
                        rg_plan* plan, rg_layout_info* info);
 
+/* Diagnostic, no counterpart in the reference: the sustained int8 MFMA rate of the current
+ * (gfx950) device in TOP/s, measured with a kernel that keeps its operands in registers
+ * (no memory traffic) for about a millisecond. dense = 1: random operand bytes, the
+ * practical ceiling of the contraction under the device's power limit; dense = 0: zero
+ * operands. Allocates a few KiB of device memory and synchronises its own stream. */
+int rg_measure_mfma_int8_rate(int dense, double* tops);
+
 #ifdef __cplusplus
 }
 #endif
