@@ -107,6 +107,17 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
         const int nsteps = L.Kp / STEP_K;
         const int min_split = ceil_div(nsteps, max_steps_per_part(S));
         int split = std::max(split_k, min_split);
+        if (split_k == 1) {
+            // Default split: when the output tiles fill at most half of the GPU's block slots
+            // (compute units x resident blocks, from the block's LDS ring), split K (int64
+            // partials, summed exactly) up to the slot count, keeping >= 2 stages per part.
+            const long long tiles = (long long)(L.Mp / (64 * ti)) * (L.Np / (64 * tj));
+            const int lds_bytes = 3 * (2 * ti + 2 * tj) * 2 * S * PANEL_BYTES;
+            const int per_cu = std::max(1, std::min(2, (160 * 1024) / lds_bytes));
+            const long long slots = (long long)std::max(1, dev.num_cus) * per_cu;
+            if (2 * tiles <= slots)
+                split = std::max(split, (int)std::min<long long>(slots / tiles, std::max(1, nsteps / 2)));
+        }
         L.split = std::min(split, nsteps);
         L.has_partial = L.split > 1;
     }

@@ -39,7 +39,8 @@ enum {
  * (128x128, 128x64, 64x128 or 64x64) forces that tile; anything else lets the
  * planner choose. tile_k is ignored. */
 typedef struct rg_config {
-    int split_k;  /* >= 1; raised automatically when needed for exact int32 sums */
+    int split_k;  /* >= 1; raised when needed for exact int32 sums, and from the default 1
+                     when the output tiles alone cannot occupy the GPU */
     int tile_m;   /* default 16 */
     int tile_n;   /* default 16 */
     int tile_k;   /* default 32, ignored */

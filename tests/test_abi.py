@@ -109,16 +109,36 @@ def test_tile_hints(tm, tn):
 @pytest.mark.parametrize("S,limit", [(1, 133120), (2, 132096), (3, 105472)])
 def test_split_raised_for_exact_int32(S, limit):
     """Each part spans at most floor((2^31-1) / level_bound / 64) * 64 values of k."""
-    p, _ = _plan(64, 64, limit, slices=S)
+    big = 4096  # enough output tiles to occupy 256 compute units: no occupancy split
+    p, _ = _plan(big, big, limit, slices=S)
     assert p.split_k == 1
-    p, _ = _plan(64, 64, limit + 64, slices=S)
+    p, _ = _plan(big, big, limit + 64, slices=S)
     assert p.split_k == 2
-    p, _ = _plan(64, 64, 3 * limit, slices=S, split_k=1)
+    p, _ = _plan(big, big, 3 * limit, slices=S, split_k=1)
     assert p.split_k == 3
 
 
+def test_default_split_fills_the_gpu():
+    """With the default split_k = 1, few output tiles get a K split (>= 2 stages per part);
+    an explicit split_k is honoured; one-stage K is never split."""
+    p, _ = _plan(1024, 64, 1024)          # 16 tiles of 64x64 (2 per CU), 16 stages of 64
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 8)
+    p, _ = _plan(64, 64, 65536)           # 1 tile, 1024 stages: up to 512 block slots
+    assert p.split_k == 512
+    p, _ = _plan(1024, 768, 768)          # 192 tiles of 64x64 <= 512 / 2 slots
+    assert p.split_k == 2
+    p, _ = _plan(1024, 2304, 768)         # 144 tiles of 128x128 (1 per CU): more than half
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
+    p, _ = _plan(1024, 1024, 64)          # one stage only
+    assert p.split_k == 1
+    p, _ = _plan(1024, 64, 1024, split_k=2)
+    assert p.split_k == 2
+    p, _ = _plan(4096, 4096, 4096)        # 1024 tiles of 128x128
+    assert p.split_k == 1
+
+
 def test_split_clamped_to_k_steps():
-    p, _ = _plan(64, 64, 100, split_k=64)
+    p, _ = _plan(4096, 4096, 100, split_k=64)
     assert p.split_k == 2  # Kp = 128 -> two stages of 64
     p, _ = _plan(64, 64, 7, split_k=64, algo=rg.Algo.Reference)
     assert p.split_k == 7  # the reference path clamps split to K
