@@ -1,4 +1,5 @@
-"""ctypes bindings of librepro_gemm.so (the C ABI in include/repro_gemm.h).
+"""ctypes bindings of librepro_gemm.so (the C ABI in include/repro_gemm.h and
+include/repro_sum.h).
 
 The library must have been built (bit_reproducible_training_amd._build.build(), or
 __graft_entry__.build()). There is no fallback: if the library is missing or does
@@ -53,7 +54,16 @@ class rg_layout_info(ctypes.Structure):
     ]
 
 
-# Every symbol declared in include/repro_gemm.h, with its ctypes signature.
+class rg_sum_config(ctypes.Structure):
+    _fields_ = [("chunks", ctypes.c_int), ("mean", ctypes.c_int)]
+
+
+class rg_sum_plan(ctypes.Structure):
+    _fields_ = [("chunks", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t)]
+
+
+# Every symbol declared in include/repro_gemm.h and include/repro_sum.h, with its ctypes
+# signature.
 _SIGNATURES = {
     "rg_config_init": (None, [ctypes.POINTER(rg_config)]),
     "rg_make_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -75,6 +85,19 @@ _SIGNATURES = {
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),
                                           ctypes.POINTER(rg_layout_info)]),
+    "rg_sum_config_init": (None, [ctypes.POINTER(rg_sum_config)]),
+    "rg_make_sum_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.POINTER(rg_sum_config), ctypes.POINTER(rg_sum_plan)]),
+    "rg_sum_plan_for_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.POINTER(rg_sum_config), ctypes.c_int,
+                                              ctypes.POINTER(rg_sum_plan)]),
+    "rg_sum_fp32_ws": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.POINTER(rg_sum_config),
+                                      ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rg_sum_fp32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int, ctypes.POINTER(rg_sum_config), ctypes.c_void_p]),
+    "rg_scan_finite": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_int, ctypes.c_void_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

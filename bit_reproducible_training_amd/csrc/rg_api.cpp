@@ -155,6 +155,8 @@ struct DevCache {
 };
 DevCache g_dev[64];
 
+}  // namespace
+
 int query_device(DeviceInfo* info) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -175,6 +177,8 @@ int query_device(DeviceInfo* info) {
     }
     return hipSuccess;
 }
+
+namespace {
 
 int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L) {
     if (!cfg) return hipErrorInvalidValue;

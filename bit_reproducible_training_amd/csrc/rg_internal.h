@@ -39,6 +39,9 @@ struct DeviceInfo {
     int num_cus;
 };
 
+// Architecture and compute-unit count of the current device (cached per device).
+int query_device(DeviceInfo* info);
+
 // Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported).
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
                 bool ta, bool tb, const DeviceInfo& dev, Layout* L);

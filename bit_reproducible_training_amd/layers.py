@@ -1,0 +1,127 @@
+"""Reproducible layers as custom autograd functions, on the MI355X kernels.
+
+Mirrors repro_torch/repro_torch/layers.py:1-100 (set_slices, get_slices, FiniteGuard,
+guard, name_layers, Linear): same names, argument meaning, results and errors. Every
+product goes through the reproducible GEMM (C = round(exact sum of 21-bit products) at the
+default S = 3), every bias gradient through the exact sum, so a training step gives the same
+bits on every run and every GPU that runs these kernels, and the same bits as the reference.
+GPU tensors only: the kernels have no CPU path.
+"""
+import torch
+
+from .repro_gemm import gemm
+from .repro_sum import exact_sum, scan_finite
+
+_slices = 3
+
+
+def set_slices(s):
+    """Sets S for every GEMM: 7*S-bit inputs (21 bits at the default S = 3)."""
+    global _slices
+    if s not in (1, 2, 3):
+        raise ValueError("slices must be 1, 2 or 3")
+    _slices = s
+
+
+def get_slices():
+    return _slices
+
+
+class FiniteGuard:
+    """Stops training with a clear error once a NaN or infinity reaches a GEMM.
+
+    The integer conversion inside the GEMM is undefined for such values, so results past that
+    point could differ between machines (layers.py:21-27). Scans are queued on the stream with
+    the operation and need no synchronisation; check() reads the flag once per step, so the
+    error arrives at the same step everywhere.
+    """
+
+    _NONE = 2 ** 31 - 1
+
+    def __init__(self):
+        self._names = []
+        self._ids = {}
+        self._flag = None
+
+    def _id(self, name):
+        if name not in self._ids:
+            self._ids[name] = len(self._names)
+            self._names.append(name)
+        return self._ids[name]
+
+    def scan(self, x, name):
+        if self._flag is None or self._flag.device != x.device:
+            self._flag = torch.full((1,), self._NONE, dtype=torch.int32, device=x.device)
+        scan_finite(x, self._flag, self._id(name))
+
+    def check(self, step=None):
+        """Raises FloatingPointError naming the first operation (in order of first use) that
+        saw a NaN or infinity since the guard was created or reset."""
+        if self._flag is None:
+            return
+        found = int(self._flag.item())
+        if found != self._NONE:
+            where = "" if step is None else " at step %d" % step
+            raise FloatingPointError("non-finite value reached %s%s" % (self._names[found], where))
+
+    def reset(self):
+        """Clears the flag (a fill kernel on the flag's stream), keeping the names."""
+        if self._flag is not None:
+            self._flag.fill_(self._NONE)
+
+
+_guard = FiniteGuard()
+
+
+def guard():
+    return _guard
+
+
+def name_layers(model, prefix=""):
+    """Names layers after their place in the model, for error messages."""
+    for name, m in model.named_modules():
+        if isinstance(m, Linear):
+            m.repro_name = prefix + name
+    return model
+
+
+class _LinearFn(torch.autograd.Function):
+    """y = x W^T + b; dX = dY W, dW = dY^T X (reproducible GEMMs), db = exact column sum of
+    dY (layers.py:70-93)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, name):
+        ctx.save_for_backward(x, weight)
+        ctx.name = name
+        _guard.scan(x, name + " input")
+        _guard.scan(weight, name + " weight")
+        m, k, n = x.shape[0], weight.shape[1], weight.shape[0]
+        y = gemm(x, weight, m, n, k, False, True, _slices)
+        return y + bias if bias is not None else y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        _guard.scan(dy, ctx.name + " gradient")
+        m, k, n = x.shape[0], weight.shape[1], weight.shape[0]
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = gemm(dy, weight, m, k, n, False, False, _slices)
+        if ctx.needs_input_grad[1]:
+            dw = gemm(dy, x, n, k, m, True, False, _slices)
+        if ctx.needs_input_grad[2]:
+            db = exact_sum(dy, m, n, 1, False)
+        return dx, dw, db, None
+
+
+class Linear(torch.nn.Linear):
+    """torch.nn.Linear with reproducible forward and backward (layers.py:96-100). Input is
+    [batch, in_features] float32 on the GPU."""
+
+    repro_name = "linear"
+
+    def forward(self, x):
+        return _LinearFn.apply(x, self.weight, self.bias, self.repro_name)
+
+
+__all__ = ["FiniteGuard", "Linear", "get_slices", "guard", "name_layers", "set_slices"]

@@ -37,6 +37,8 @@ _SIG = {
     "oracle_gen_adversarial": (None, [_vp, _i, _i, _u64, _i, _i]),
     "oracle_splitmix64": (None, [_vp, _sz, _u64]),
     "oracle_fnv1a64": (_u64, [_vp, _sz, _u64]),
+    "oracle_exact_sum": (None, [_vp, _vp, _i, _i, _i, _i]),
+    "oracle_has_nonfinite": (_i, [_vp, _sz]),
 }
 
 _REF_SIG = {
@@ -44,6 +46,7 @@ _REF_SIG = {
     "ref_fixed_point": (_i, [_f, _i, _i]),
     "ref_round_to_float": (_f, [ctypes.c_int64, _i]),
     "ref_cpu_gemm": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i]),
+    "ref_exact_sum": (None, [_vp, _vp, _i, _i, _i, _i]),
 }
 
 
@@ -195,3 +198,27 @@ def ref_cpu_gemm(A, B, M, N, K, ta=False, tb=False, S=3):
     C = np.empty((M, N), np.float32)
     ref.ref_cpu_gemm(_ptr(A), _ptr(B), _ptr(C), M, N, K, int(bool(ta)), int(bool(tb)), S)
     return C
+
+
+def exact_sum(x, A, B, C, mean=False):
+    """out[b] = exact sum over a, c of x[a][b][c] rounded once (or the mean)."""
+    x = np.ascontiguousarray(x, np.float32)
+    assert x.size == A * B * C
+    out = np.empty(int(B), np.float32)
+    lib.oracle_exact_sum(_ptr(x), _ptr(out), int(A), int(B), int(C), int(bool(mean)))
+    return out
+
+
+def has_nonfinite(x):
+    x = np.ascontiguousarray(x, np.float32)
+    return bool(lib.oracle_has_nonfinite(_ptr(x), x.size))
+
+
+def ref_exact_sum(x, A, B, C, mean=False):
+    """The reference's own accumulator (oracle/_ref), or None when it was not built."""
+    if ref is None:
+        return None
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(int(B), np.float32)
+    ref.ref_exact_sum(_ptr(x), _ptr(out), int(A), int(B), int(C), int(bool(mean)))
+    return out

@@ -1,10 +1,12 @@
 // C-linkage entry points over the reference's own CPU implementation, compiled from the
-// reference headers where they lie (-I <reference>/repro_gemm_cuda); nothing is copied.
+// reference headers where they lie (-I <reference>/repro_gemm_cuda, -I <reference>/repro_sum_cuda);
+// nothing is copied.
 // TEST INFRASTRUCTURE ONLY: used by tests/ to pin oracle/repro_oracle.c against the
 // reference itself, and by bench.py's cpu_baseline leg as the timed CPU path.
 #include <cstdint>
 
 #include "repro_gemm_cpu.h"  // repro_gemm_cuda/repro_gemm_cpu.h:25-51 (includes the math header)
+#include "repro_sum_math.cuh"  // repro_sum_cuda/repro_sum_math.cuh (header-only superaccumulator)
 
 extern "C" {
 
@@ -18,6 +20,19 @@ float ref_round_to_float(int64_t T, int E) { return repro_gemm::round_to_float(T
 void ref_cpu_gemm(const float* A, const float* B, float* C, int M, int N, int K, int ta, int tb,
                   int S) {
     repro_gemm::cpu_gemm(A, B, C, M, N, K, ta != 0, tb != 0, S);
+}
+
+// The CPU branch of repro_torch/src/bindings.cpp:69-91 (exact_sum), single-threaded, on the
+// reference's own accumulator functions.
+void ref_exact_sum(const float* x, float* out, int A, int B, int C, int mean) {
+    const uint32_t divisor = mean ? (uint32_t)((int64_t)A * C) : 1u;
+    for (int b = 0; b < B; ++b) {
+        int64_t acc[repro_sum::LIMBS] = {};
+        int nf = 0;
+        for (int a = 0; a < A; ++a)
+            for (int c = 0; c < C; ++c) repro_sum::acc_add(acc, 1, x[((size_t)a * B + b) * C + c], nf);
+        out[b] = repro_sum::finalize(acc, 1, divisor, nf);
+    }
 }
 
 }  // extern "C"

@@ -478,3 +478,101 @@ uint64_t oracle_fnv1a64(const void* data, size_t n, uint64_t h) {
     }
     return h;
 }
+
+/* ------------------------------------------------------------------------- */
+/* Exact sum (superaccumulator), repro_sum_cuda/repro_sum_math.cuh            */
+/* ------------------------------------------------------------------------- */
+
+#define SUM_LIMBS 10
+
+/* Adds x as two integer addends at its limb pair; 0 for NaN/Inf
+ * (repro_sum_math.cuh:66-91). Limb l weighs 2^(32 l - 149). */
+static int sum_add(int64_t* acc, float x) {
+    uint32_t b = f2u(x), e = (b >> 23) & 0xFFu, f = b & 0x7FFFFFu;
+    if (e == 0xFFu) return 0;
+    uint64_t m = e ? (uint64_t)(f | 0x800000u) : (uint64_t)f;
+    int sh = e ? (int)e - 1 : 0;
+    uint64_t v = m << (sh & 31);
+    int64_t lo = (int64_t)(v & 0xFFFFFFFFull), hi = (int64_t)(v >> 32);
+    if (b >> 31) { lo = -lo; hi = -hi; }
+    acc[sh >> 5] += lo;
+    acc[(sh >> 5) + 1] += hi;
+    return 1;
+}
+
+/* Carries with floor division by 2^32 (repro_sum_math.cuh:93-100). */
+static void sum_normalize(int64_t* t) {
+    for (int l = 0; l < SUM_LIMBS - 1; ++l) {
+        int64_t c = t[l] >> 32;
+        t[l] -= c * 4294967296LL;
+        t[l + 1] += c;
+    }
+}
+
+/* Exact value / divisor rounded once, nearest-even, by long division and guard/sticky
+ * bits (repro_sum_math.cuh:102-157). */
+static float sum_finalize(int64_t* t, uint32_t divisor, int nonfinite) {
+    if (nonfinite) return u2f(0x7FC00000u);
+    sum_normalize(t);
+    int neg = t[SUM_LIMBS - 1] < 0;
+    if (neg) {
+        for (int l = 0; l < SUM_LIMBS; ++l) t[l] = -t[l];
+        sum_normalize(t);
+    }
+    uint32_t q[SUM_LIMBS];
+    uint64_t rem = 0;
+    for (int l = SUM_LIMBS - 1; l >= 0; --l) {
+        uint64_t cur = (rem << 32) | (uint64_t)(uint32_t)t[l];
+        q[l] = (uint32_t)(cur / divisor);
+        rem = cur % divisor;
+    }
+    int top = SUM_LIMBS - 1;
+    while (top >= 0 && q[top] == 0) --top;
+    float r;
+    if (top < 0) {
+        if (rem == 0) return 0.0f;
+        r = (2 * rem > divisor) ? u2f(1u) : 0.0f;       /* 2^-149 or 0 (a tie is even: 0) */
+        return neg ? -r : r;
+    }
+    int p = 32 * top + 31 - __builtin_clz(q[top]);
+    int shift = p > 23 ? p - 23 : 0;
+    int kl = shift >> 5;
+    uint64_t two = (uint64_t)q[kl] | (kl + 1 < SUM_LIMBS ? (uint64_t)q[kl + 1] << 32 : 0u);
+    uint32_t kept = (uint32_t)(two >> (shift & 31)) & 0xFFFFFFu;
+    int up;
+    if (shift > 0) {
+        int g = shift - 1;
+        int guard = (q[g >> 5] >> (g & 31)) & 1u;
+        int lower = rem != 0;
+        for (int l = 0; l < (g >> 5); ++l) lower = lower || q[l] != 0;
+        lower = lower || (q[g >> 5] & ((1u << (g & 31)) - 1u)) != 0;
+        up = guard && (lower || (kept & 1u));
+    } else {
+        up = 2 * rem > divisor || (2 * rem == divisor && (kept & 1u));
+    }
+    kept += (uint32_t)up;
+    r = ldexpf((float)kept, shift - 149);
+    return neg ? -r : r;
+}
+
+/* out[b] = exact sum over a, c of x[a][b][c], rounded once; divided exactly by A*C when
+ * mean (repro_torch/src/bindings.cpp:69-91, CPU branch). */
+void oracle_exact_sum(const float* x, float* out, int A, int B, int C, int mean) {
+    uint32_t divisor = mean ? (uint32_t)((int64_t)A * C) : 1u;
+    for (int b = 0; b < B; ++b) {
+        int64_t acc[SUM_LIMBS] = {0};
+        int nonfinite = 0;
+        for (int a = 0; a < A; ++a)
+            for (int c = 0; c < C; ++c)
+                if (!sum_add(acc, x[((size_t)a * B + b) * C + c])) nonfinite = 1;
+        out[b] = sum_finalize(acc, divisor, nonfinite);
+    }
+}
+
+/* 1 if x holds a NaN or infinity (exponent field all ones), else 0
+ * (the test of repro_torch/src/kernels.cu:10-14). */
+int oracle_has_nonfinite(const float* x, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if ((f2u(x[i]) & 0x7F800000u) == 0x7F800000u) return 1;
+    return 0;
+}

@@ -26,6 +26,11 @@
  *                          brute force with Python integers on tiny shapes, and _ref.
  *   oracle_gen_normal      the 21 recorded input hashes (same lines, in= column).
  *   oracle_fnv1a64         the FNV-1a-64 published test vectors.
+ *   oracle_exact_sum       exact rational sums (Python fractions) rounded to binary32 by an
+ *                          integer-only rounding, on random, cancelling, tie, subnormal,
+ *                          overflow and non-finite inputs, sum and mean; oracle/_ref (the
+ *                          reference's repro_sum_math.cuh compiled here).
+ *   oracle_has_nonfinite   numpy.isfinite on the same arrays.
  */
 #ifndef REPRO_ORACLE_H
 #define REPRO_ORACLE_H
@@ -95,6 +100,14 @@ void oracle_gen_uniform_pm(float* out, size_t n, float bound, uint64_t seed, uin
 void oracle_gen_adversarial(float* out, int rows, int cols, uint64_t seed, int pair_rows, int negate);
 /* Raw stream: n successive SplitMix64 outputs. */
 void oracle_splitmix64(uint64_t* out, size_t n, uint64_t seed);
+
+/* out[b] = exact sum over a, c of x[a][b][c] (x is [A][B][C] row-major), rounded once to
+ * float32 nearest-even, or the exact sum / (A*C) when mean; NaN if any summand is NaN or
+ * infinite; an exactly zero sum is +0.0 (repro_sum_cuda/repro_sum_math.cuh:66-157,
+ * repro_torch/src/bindings.cpp:69-91). */
+void oracle_exact_sum(const float* x, float* out, int A, int B, int C, int mean);
+/* 1 if x[0..n) holds a NaN or infinity (repro_torch/src/kernels.cu:10-14). */
+int oracle_has_nonfinite(const float* x, size_t n);
 
 /* FNV-1a 64 over raw bytes, chained from h (repro_gemm_cuda/repro_test_util.h:20-24). */
 uint64_t oracle_fnv1a64(const void* data, size_t n, uint64_t h);

@@ -1,5 +1,4 @@
-"""The C ABI library on the host: it loads, exports every symbol include/repro_gemm.h
-declares, and its planner behaves as the reference's make_plan does
+"""The C ABI library on the host: it loads, exports every symbol include/*.h declares, and its planner behaves as the reference's make_plan does
 (repro_gemm_cuda/repro_gemm.cu:390-439, 503-509). No kernel is launched here."""
 import ctypes
 import math
@@ -15,9 +14,11 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared_symbols():
-    with open(os.path.join(REPO, "include", "repro_gemm.h")) as f:
-        text = f.read()
-    return sorted(set(re.findall(r"\b(rg_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for header in ("repro_gemm.h", "repro_sum.h"):
+        with open(os.path.join(REPO, "include", header)) as f:
+            names |= set(re.findall(r"\b(rg_[a-z0-9_]+)\s*\(", f.read()))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
