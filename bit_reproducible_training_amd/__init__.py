@@ -1,10 +1,11 @@
 """MI355X (gfx950) reproducible FP32 GEMM: int8 slice split, int8 MFMA contraction,
 exact recombination. Bit-identical to the CPU definition on every input. Around it: the
-exact (superaccumulator) sum and non-finite scan its layers need, and the reproducible
-Linear layer (autograd) built on both.
+reproducible convolution (forward and both gradients) on the same contraction, the exact
+(superaccumulator) sum and non-finite scan the layers need, and the reproducible Linear and
+Conv2d layers (autograd) built on them.
 
-The compute path is librepro_gemm.so (HIP kernels + C ABI, include/repro_gemm.h and
-include/repro_sum.h); this package is its Python host mirror. Importing it fails if the
+The compute path is librepro_gemm.so (HIP kernels + C ABI, include/repro_gemm.h,
+include/repro_sum.h, include/repro_conv.h); this package is its Python host mirror. Importing it fails if the
 library is not built.
 """
 from .repro_gemm import (  # noqa: F401
@@ -32,4 +33,24 @@ from .repro_sum import (  # noqa: F401
     scan_finite,
     sum_plan_for_device,
 )
-from .layers import FiniteGuard, Linear, get_slices, guard, name_layers, set_slices  # noqa: F401
+from .repro_conv import (  # noqa: F401
+    ConvShape,
+    conv2d,
+    conv2d_grad_input,
+    conv2d_grad_input_workspace,
+    conv2d_grad_weight,
+    conv2d_grad_weight_workspace,
+    conv2d_workspace,
+    repro_conv2d_grad_input_ws,
+    repro_conv2d_grad_weight_ws,
+    repro_conv2d_ws,
+)
+from .layers import (  # noqa: F401
+    Conv2d,
+    FiniteGuard,
+    Linear,
+    get_slices,
+    guard,
+    name_layers,
+    set_slices,
+)

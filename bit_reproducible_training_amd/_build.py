@@ -17,7 +17,7 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "librepro_gemm.so")
 
-SOURCES = ["rg_slice.hip", "rg_contract.hip", "rg_probe.hip", "rg_sum.hip", "rg_api.cpp"]
+SOURCES = ["rg_slice.hip", "rg_contract.hip", "rg_probe.hip", "rg_sum.hip", "rg_conv.hip", "rg_api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -1,5 +1,5 @@
-"""ctypes bindings of librepro_gemm.so (the C ABI in include/repro_gemm.h and
-include/repro_sum.h).
+"""ctypes bindings of librepro_gemm.so (the C ABI in include/repro_gemm.h,
+include/repro_sum.h and include/repro_conv.h).
 
 The library must have been built (bit_reproducible_training_amd._build.build(), or
 __graft_entry__.build()). There is no fallback: if the library is missing or does
@@ -62,8 +62,19 @@ class rg_sum_plan(ctypes.Structure):
     _fields_ = [("chunks", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t)]
 
 
-# Every symbol declared in include/repro_gemm.h and include/repro_sum.h, with its ctypes
-# signature.
+class rg_conv_shape(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int) for name in
+                ("N", "C", "H", "W", "F", "KH", "KW", "SY", "SX", "PY", "PX")]
+
+
+_CONV_WS = (ctypes.c_int, [ctypes.POINTER(rg_conv_shape), ctypes.c_int,
+                           ctypes.POINTER(ctypes.c_size_t)])
+_CONV_RUN = (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                            ctypes.POINTER(rg_conv_shape), ctypes.c_int, ctypes.c_void_p,
+                            ctypes.c_size_t, ctypes.c_void_p])
+
+# Every symbol declared in include/repro_gemm.h, include/repro_sum.h and include/repro_conv.h,
+# with its ctypes signature.
 _SIGNATURES = {
     "rg_config_init": (None, [ctypes.POINTER(rg_config)]),
     "rg_make_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -98,6 +109,13 @@ _SIGNATURES = {
                                    ctypes.c_int, ctypes.POINTER(rg_sum_config), ctypes.c_void_p]),
     "rg_scan_finite": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_int, ctypes.c_void_p]),
+    "rg_conv_shape_init": (None, [ctypes.POINTER(rg_conv_shape)]),
+    "rg_conv2d_workspace": _CONV_WS,
+    "rg_conv2d_grad_weight_workspace": _CONV_WS,
+    "rg_conv2d_grad_input_workspace": _CONV_WS,
+    "rg_conv2d_ws": _CONV_RUN,
+    "rg_conv2d_grad_weight_ws": _CONV_RUN,
+    "rg_conv2d_grad_input_ws": _CONV_RUN,
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -61,11 +61,11 @@ void choose_chunks(int R, int K, bool strided, int* nch, int* kch) {
 }  // namespace
 
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
-                bool ta, bool tb, const DeviceInfo& dev, Layout* Lp) {
+                bool ta, bool tb, const DeviceInfo& dev, Layout* Lp, bool raw, bool gemm_bound) {
     if (M <= 0 || N <= 0 || K <= 0 || split_k <= 0) return hipErrorInvalidValue;
     if (S < 1 || S > 3) return hipErrorInvalidValue;
     const double d = max_fixed_point(S);
-    if ((double)K * d * d > std::ldexp(1.0, 62)) return hipErrorInvalidValue;
+    if (gemm_bound && (double)K * d * d > std::ldexp(1.0, 62)) return hipErrorInvalidValue;
     if (algo < RG_ALGO_AUTO || algo > RG_ALGO_TENSOR_CORE) return hipErrorInvalidValue;
 
     Layout L;
@@ -119,7 +119,7 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
                 split = std::max(split, (int)std::min<long long>(slots / tiles, std::max(1, nsteps / 2)));
         }
         L.split = std::min(split, nsteps);
-        L.has_partial = L.split > 1;
+        L.has_partial = L.split > 1 || raw;
     }
 
     choose_chunks(M, K, L.a_strided, &L.nch_a, &L.kch_a);
@@ -178,9 +178,8 @@ int query_device(DeviceInfo* info) {
     return hipSuccess;
 }
 
-namespace {
-
-int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L) {
+int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L, bool raw,
+                              bool gemm_bound) {
     if (!cfg) return hipErrorInvalidValue;
     DeviceInfo dev{false, 0};
     if (cfg->algo != RG_ALGO_REFERENCE) {
@@ -188,10 +187,63 @@ int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout*
         if (e != hipSuccess) return e;
     }
     return plan_layout(M, N, K, cfg->split_k, cfg->tile_m, cfg->tile_n, cfg->algo, cfg->slices,
-                       cfg->trans_a != 0, cfg->trans_b != 0, dev, L);
+                       cfg->trans_a != 0, cfg->trans_b != 0, dev, L, raw, gemm_bound);
 }
 
-}  // namespace
+int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char* base,
+                hipStream_t stream, void* const* stage_events, const GemmOptions& opt) {
+    auto record = [&](int i) {
+        if (stage_events) (void)hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream);
+    };
+    void* qa = base + L.qa;
+    void* qb = base + L.qb;
+    int* ea = reinterpret_cast<int*>(base + L.ea);
+    int* eb = reinterpret_cast<int*>(base + L.eb);
+    float* pma = reinterpret_cast<float*>(base + L.pma);
+    float* pmb = reinterpret_cast<float*>(base + L.pmb);
+    int64_t* part = L.has_partial ? reinterpret_cast<int64_t*>(base + L.part) : nullptr;
+    const bool i32 = L.algo == RG_ALGO_REFERENCE;
+
+    auto desc = [&](const float* src, int R, int Rp, bool strided, int nch, int kch, float* pm,
+                    void* out, int* expo) {
+        SliceDesc d;
+        d.src = src;
+        d.R = R;
+        d.K = L.K;
+        d.Rp = Rp;
+        d.Kp = L.Kp;
+        d.strided = strided ? 1 : 0;
+        const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+        d.vec = aligned && (strided ? (R % 4 == 0) : (L.K % 4 == 0)) ? 1 : 0;
+        d.nch = nch;
+        d.kch = kch;
+        d.pmax = pm;
+        d.out = out;
+        d.expo = expo;
+        slice_grid(d);
+        return d;
+    };
+    const SliceDesc da = desc(A, L.M, L.Mp, L.a_strided, L.nch_a, L.kch_a, pma, qa, ea);
+    const SliceDesc db = desc(B, L.N, L.Np, L.b_strided, L.nch_b, L.kch_b, pmb, qb, eb);
+
+    record(0);
+    launch_absmax(da, db, stream);
+    if (opt.group_a > 0) launch_group_max(da, opt.group_a, stream);
+    if (opt.group_b > 0) launch_group_max(db, opt.group_b, stream);
+    launch_split(da, db, L.S, i32, stream);
+    record(1);
+    if (i32)
+        launch_contract_reference(L, static_cast<const int32_t*>(qa),
+                                  static_cast<const int32_t*>(qb), part, stream);
+    else
+        launch_contract_mfma(L, static_cast<const int8_t*>(qa), static_cast<const int8_t*>(qb),
+                             ea, eb, C, part, stream);
+    record(2);
+    if (L.has_partial && !opt.raw) launch_reduce_round(L, part, ea, eb, C, stream);
+    record(3);
+    return hipGetLastError();
+}
+
 }  // namespace rg
 
 extern "C" {
@@ -266,63 +318,15 @@ int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_inf
 }
 
 int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int K,
-                    const rg_config* cfg, void* workspace, size_t workspace_bytes, void* stream_,
+                    const rg_config* cfg, void* workspace, size_t workspace_bytes, void* stream,
                     void* const* stage_events) {
     if (!A || !B || !C) return hipErrorInvalidValue;
     rg::Layout L;
     int e = rg::layout_for_current_device(M, N, K, cfg, &L);
     if (e != hipSuccess) return e;
     if (!workspace || workspace_bytes < L.total) return hipErrorInvalidValue;
-    hipStream_t stream = static_cast<hipStream_t>(stream_);
-    auto record = [&](int i) {
-        if (stage_events) (void)hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream);
-    };
-    char* base = static_cast<char*>(workspace);
-    void* qa = base + L.qa;
-    void* qb = base + L.qb;
-    int* ea = reinterpret_cast<int*>(base + L.ea);
-    int* eb = reinterpret_cast<int*>(base + L.eb);
-    float* pma = reinterpret_cast<float*>(base + L.pma);
-    float* pmb = reinterpret_cast<float*>(base + L.pmb);
-    int64_t* part = L.has_partial ? reinterpret_cast<int64_t*>(base + L.part) : nullptr;
-    const bool i32 = L.algo == RG_ALGO_REFERENCE;
-
-    auto desc = [&](const float* src, int R, int Rp, bool strided, int nch, int kch, float* pm,
-                    void* out, int* expo) {
-        rg::SliceDesc d;
-        d.src = src;
-        d.R = R;
-        d.K = K;
-        d.Rp = Rp;
-        d.Kp = L.Kp;
-        d.strided = strided ? 1 : 0;
-        const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
-        d.vec = aligned && (strided ? (R % 4 == 0) : (K % 4 == 0)) ? 1 : 0;
-        d.nch = nch;
-        d.kch = kch;
-        d.pmax = pm;
-        d.out = out;
-        d.expo = expo;
-        rg::slice_grid(d);
-        return d;
-    };
-    const rg::SliceDesc da = desc(A, M, L.Mp, L.a_strided, L.nch_a, L.kch_a, pma, qa, ea);
-    const rg::SliceDesc db = desc(B, N, L.Np, L.b_strided, L.nch_b, L.kch_b, pmb, qb, eb);
-
-    record(0);
-    rg::launch_absmax(da, db, stream);
-    rg::launch_split(da, db, L.S, i32, stream);
-    record(1);
-    if (i32)
-        rg::launch_contract_reference(L, static_cast<const int32_t*>(qa),
-                                      static_cast<const int32_t*>(qb), part, stream);
-    else
-        rg::launch_contract_mfma(L, static_cast<const int8_t*>(qa), static_cast<const int8_t*>(qb),
-                                 ea, eb, C, part, stream);
-    record(2);
-    if (L.has_partial) rg::launch_reduce_round(L, part, ea, eb, C, stream);
-    record(3);
-    return hipGetLastError();
+    return rg::gemm_launch(A, B, C, L, static_cast<char*>(workspace),
+                           static_cast<hipStream_t>(stream), stage_events, rg::GemmOptions());
 }
 
 int rg_gemm_fp32(const float* A, const float* B, float* C, int M, int N, int K,

@@ -13,7 +13,8 @@
 // accumulators of one output sit in the same lane and register index, so the epilogue
 // combines them in int64 without any data exchange:
 //     T = sum_L acc_L * 2^(7 (2S-2-L)) = sum_k X[r,k] * Y[c,k]   (exact)
-// and either rounds T once to FP32 (one part) or stores it as an int64 partial.
+// and either rounds T once to FP32 (no partial buffer: one part) or stores it as an int64
+// partial (split-K, or a caller that wants the exact integers).
 // Integer addition is associative, so the tile shape, the split and the order of k
 // never change T.
 #include "rg_internal.h"
@@ -166,7 +167,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #pragma unroll
                     for (int l = 0; l < L; ++l)
                         t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
-                    if (split == 1)
+                    if (partial == nullptr)
                         C[(size_t)row * N + col] = round_to_float(t, eA[row] + ec);
                     else
                         partial[((size_t)part * M + row) * N + col] = t;

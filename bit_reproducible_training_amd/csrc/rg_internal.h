@@ -3,6 +3,8 @@
 // host API of librepro_gemm.so. Nothing here is part of the public ABI.
 #include <hip/hip_runtime.h>
 
+#include "repro_gemm.h"
+
 #include <cstddef>
 #include <cstdint>
 
@@ -42,9 +44,14 @@ struct DeviceInfo {
 // Architecture and compute-unit count of the current device (cached per device).
 int query_device(DeviceInfo* info);
 
-// Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported).
+// Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported). raw: keep
+// the exact int64 sums T (the partial buffer [split][M][N], summed by the caller) instead of
+// rounding them to C. gemm_bound: apply the reference GEMM's K bound (K * max|X|^2 <= 2^62
+// with max|X| the largest digit-split value); callers with their own exactness bound (the
+// convolution's, on the clamped |X| <= 127*128^(S-1)) pass false.
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
-                bool ta, bool tb, const DeviceInfo& dev, Layout* L);
+                bool ta, bool tb, const DeviceInfo& dev, Layout* L, bool raw = false,
+                bool gemm_bound = true);
 
 // One operand of the slice split: op(X) has R rows of K values; `strided` when row r is
 // read along k with stride R (element (r, k) at src[k*R + r]), else src[r*K + k].
@@ -63,9 +70,30 @@ struct SliceDesc {
 // Fills max_blocks / split_blocks of d.
 void slice_grid(SliceDesc& d);
 
+// Options of the launch sequence beyond the reference's GEMM, for the convolution's input
+// gradient: group_a > 0 gives every group of group_a consecutive rows of op(A) one scale (the
+// largest magnitude in the group; group_a >= M: one scale for all), likewise group_b for the
+// columns of op(B); raw keeps the exact int64 sums in the workspace's partial buffer.
+struct GemmOptions {
+    int group_a = 0;
+    int group_b = 0;
+    bool raw = false;
+};
+
+// Layout for the current device (queried once per device and cached).
+int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L,
+                              bool raw = false, bool gemm_bound = true);
+
+// The launch sequence of one GEMM on `stream` (slicing, contraction, final rounding unless
+// raw) into a workspace laid out by L at `base`. events: NULL or 4 hipEvent_t.
+int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char* base,
+                hipStream_t stream, void* const* events, const GemmOptions& opt);
+
 // Kernel launchers (asynchronous on `stream`).
 void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream);
 void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream);
+// Replaces the partial row maxima of d by the maximum over each group of `group` rows.
+void launch_group_max(const SliceDesc& d, int group, hipStream_t stream);
 void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
                           const int* eb, float* C, int64_t* partial, hipStream_t stream);
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,

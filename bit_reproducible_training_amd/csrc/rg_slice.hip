@@ -327,6 +327,35 @@ void slice_grid(SliceDesc& d) {
     d.split_blocks = (long long)(d.Rp / PANEL_ROWS) * ((npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G));
 }
 
+// Group scales: every row of each group of `group` consecutive rows gets the group's largest
+// magnitude. Block g reduces the partial maxima pmax[c][r] of its rows over every chunk c,
+// then writes the maximum back to all of them, so the split sees one maximum per group.
+__global__ void __launch_bounds__(256)
+group_max_kernel(float* __restrict__ pmax, int R, int Rp, int nch, int group) {
+    __shared__ float red[4];
+    const int r0 = blockIdx.x * group;
+    const int rows = min(R, r0 + group) - r0;
+    const long long n = (long long)rows * nch;
+    float m = 0.0f;
+    for (long long i = threadIdx.x; i < n; i += 256) {
+        const int c = (int)(i / rows), r = r0 + (int)(i - (long long)c * rows);
+        m = fmaxf(m, pmax[(size_t)c * Rp + r]);
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (long long i = threadIdx.x; i < n; i += 256) {
+        const int c = (int)(i / rows), r = r0 + (int)(i - (long long)c * rows);
+        pmax[(size_t)c * Rp + r] = m;
+    }
+}
+
+void launch_group_max(const SliceDesc& d, int group, hipStream_t stream) {
+    const int g = group >= d.R ? d.R : group;
+    group_max_kernel<<<(unsigned)((d.R + g - 1) / g), 256, 0, stream>>>(d.pmax, d.R, d.Rp, d.nch, g);
+}
+
 void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream) {
     absmax_kernel<<<(unsigned)(a.max_blocks + b.max_blocks), 256, 0, stream>>>(a, b);
 }

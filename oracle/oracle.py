@@ -39,6 +39,9 @@ _SIG = {
     "oracle_fnv1a64": (_u64, [_vp, _sz, _u64]),
     "oracle_exact_sum": (None, [_vp, _vp, _i, _i, _i, _i]),
     "oracle_has_nonfinite": (_i, [_vp, _sz]),
+    "oracle_conv2d": (None, [_vp, _vp, _vp, _vp, _i]),
+    "oracle_conv2d_grad_weight": (None, [_vp, _vp, _vp, _vp, _i]),
+    "oracle_conv2d_grad_input": (None, [_vp, _vp, _vp, _vp, _i]),
 }
 
 _REF_SIG = {
@@ -47,6 +50,9 @@ _REF_SIG = {
     "ref_round_to_float": (_f, [ctypes.c_int64, _i]),
     "ref_cpu_gemm": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i]),
     "ref_exact_sum": (None, [_vp, _vp, _i, _i, _i, _i]),
+    "ref_conv2d": (None, [_vp, _vp, _vp, _vp, _i]),
+    "ref_conv2d_grad_weight": (None, [_vp, _vp, _vp, _vp, _i]),
+    "ref_conv2d_grad_input": (None, [_vp, _vp, _vp, _vp, _i]),
 }
 
 
@@ -222,3 +228,55 @@ def ref_exact_sum(x, A, B, C, mean=False):
     out = np.empty(int(B), np.float32)
     ref.ref_exact_sum(_ptr(x), _ptr(out), int(A), int(B), int(C), int(bool(mean)))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# Convolution. shape = (N, C, H, W, F, KH, KW, SY, SX, PY, PX).
+# ---------------------------------------------------------------------------------------
+
+def conv_out_hw(shape):
+    N, C, H, W, F, KH, KW, SY, SX, PY, PX = shape
+    return (H + 2 * PY - KH) // SY + 1, (W + 2 * PX - KW) // SX + 1
+
+
+def _shape_arr(shape):
+    assert len(shape) == 11
+    return np.ascontiguousarray(shape, np.int32)
+
+
+def _conv_call(fn, a, b, out_shape, shape, S):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty(out_shape, np.float32)
+    s = _shape_arr(shape)
+    fn(_ptr(a), _ptr(b), _ptr(out), _ptr(s), int(S))
+    return out
+
+
+def conv2d(x, w, shape, S=3):
+    N, C, H, W, F = shape[:5]
+    OH, OW = conv_out_hw(shape)
+    return _conv_call(lib.oracle_conv2d, x, w, (N, F, OH, OW), shape, S)
+
+
+def conv2d_grad_weight(dy, x, shape, S=3):
+    N, C, H, W, F, KH, KW = shape[:7]
+    return _conv_call(lib.oracle_conv2d_grad_weight, dy, x, (F, C, KH, KW), shape, S)
+
+
+def conv2d_grad_input(dy, w, shape, S=3):
+    N, C, H, W = shape[:4]
+    return _conv_call(lib.oracle_conv2d_grad_input, dy, w, (N, C, H, W), shape, S)
+
+
+def ref_conv(kind, a, b, shape, S=3):
+    """The reference's own repro_conv_cpu.h (oracle/_ref): kind in fwd, dW, dX; None when
+    _ref was not built."""
+    if ref is None:
+        return None
+    N, C, H, W, F, KH, KW = shape[:7]
+    OH, OW = conv_out_hw(shape)
+    fn, out_shape = {"fwd": (ref.ref_conv2d, (N, F, OH, OW)),
+                     "dW": (ref.ref_conv2d_grad_weight, (F, C, KH, KW)),
+                     "dX": (ref.ref_conv2d_grad_input, (N, C, H, W))}[kind]
+    return _conv_call(fn, a, b, out_shape, shape, S)

@@ -576,3 +576,143 @@ int oracle_has_nonfinite(const float* x, size_t n) {
         if ((f2u(x[i]) & 0x7F800000u) == 0x7F800000u) return 1;
     return 0;
 }
+
+/* ------------------------------------------------------------------------- */
+/* Convolution, repro_conv_cuda/repro_conv_math.cuh and repro_conv_cpu.h      */
+/* ------------------------------------------------------------------------- */
+
+/* Input value at position (c, ky, kx) of window (n, oy, ox), zero in the padding
+ * (repro_conv_math.cuh:46-52). */
+static float conv_window_value(const float* x, const oracle_conv_shape* g, int n, int oy, int ox,
+                               int c, int ky, int kx) {
+    int y = oy * g->SY - g->PY + ky, xx = ox * g->SX - g->PX + kx;
+    if (y < 0 || y >= g->H || xx < 0 || xx >= g->W) return 0.0f;
+    return x[(((size_t)n * g->C + c) * g->H + y) * g->W + xx];
+}
+
+static int conv_oh(const oracle_conv_shape* g) { return (g->H + 2 * g->PY - g->KH) / g->SY + 1; }
+static int conv_ow(const oracle_conv_shape* g) { return (g->W + 2 * g->PX - g->KW) / g->SX + 1; }
+
+/* Forward (repro_conv_cpu.h:23-38, repro_conv_math.cuh:68-99): weights quantised per filter,
+ * each window per window, Y[n][f][oy][ox] = round(sum_k X * W, e_window + e_filter + e0). */
+void oracle_conv2d(const float* x, const float* w, float* out, const oracle_conv_shape* g, int S) {
+    int K = g->C * g->KH * g->KW, oh = conv_oh(g), ow = conv_ow(g), e0 = -14 * (S - 1);
+    int* Wq = (int*)malloc(sizeof(int) * (size_t)g->F * K);
+    int* eF = (int*)malloc(sizeof(int) * (size_t)g->F);
+    int* q = (int*)malloc(sizeof(int) * (size_t)K);
+    float* v = (float*)malloc(sizeof(float) * (size_t)K);
+    for (int f = 0; f < g->F; ++f) {
+        float m = 0.0f;
+        for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(w[(size_t)f * K + k]));
+        eF[f] = oracle_scale_exponent(m);
+        for (int k = 0; k < K; ++k) Wq[(size_t)f * K + k] = oracle_fixed_point(w[(size_t)f * K + k], eF[f], S);
+    }
+    for (int n = 0; n < g->N; ++n)
+        for (int oy = 0; oy < oh; ++oy)
+            for (int ox = 0; ox < ow; ++ox) {
+                float m = 0.0f;
+                for (int k = 0; k < K; ++k) {
+                    int c = k / (g->KH * g->KW), r = k % (g->KH * g->KW);
+                    v[k] = conv_window_value(x, g, n, oy, ox, c, r / g->KW, r % g->KW);
+                    m = fmaxf(m, fabsf(v[k]));
+                }
+                int e = oracle_scale_exponent(m);
+                for (int k = 0; k < K; ++k) q[k] = oracle_fixed_point(v[k], e, S);
+                for (int f = 0; f < g->F; ++f) {
+                    int64_t t = 0;
+                    for (int k = 0; k < K; ++k) t += (int64_t)q[k] * Wq[(size_t)f * K + k];
+                    out[(((size_t)n * g->F + f) * oh + oy) * ow + ox] =
+                        oracle_round_to_float(t, e + eF[f] + e0);
+                }
+            }
+    free(Wq); free(eF); free(q); free(v);
+}
+
+/* Weight gradient (repro_conv_cpu.h:40-70, repro_conv_math.cuh:101-130): dY quantised per
+ * filter, x per window position over all windows, dW[f][k] = round(sum_w D * X,
+ * e_filter + e_position + e0). */
+void oracle_conv2d_grad_weight(const float* dy, const float* x, float* dw,
+                               const oracle_conv_shape* g, int S) {
+    int K = g->C * g->KH * g->KW, oh = conv_oh(g), ow = conv_ow(g), e0 = -14 * (S - 1);
+    size_t P = (size_t)oh * ow, outn = (size_t)g->N * g->F * P;
+    int* eF = (int*)malloc(sizeof(int) * (size_t)g->F);
+    int* D = (int*)malloc(sizeof(int) * outn);
+    int* X = (int*)malloc(sizeof(int) * (size_t)g->N * P);
+    int64_t* t = (int64_t*)malloc(sizeof(int64_t) * (size_t)g->F);
+    for (int f = 0; f < g->F; ++f) {
+        float m = 0.0f;
+        for (int n = 0; n < g->N; ++n)
+            for (size_t p = 0; p < P; ++p) m = fmaxf(m, fabsf(dy[((size_t)n * g->F + f) * P + p]));
+        eF[f] = oracle_scale_exponent(m);
+    }
+    for (size_t i = 0; i < outn; ++i) D[i] = oracle_fixed_point(dy[i], eF[(i / P) % g->F], S);
+    for (int k = 0; k < K; ++k) {
+        int c = k / (g->KH * g->KW), r = k % (g->KH * g->KW), ky = r / g->KW, kx = r % g->KW;
+        float m = 0.0f;
+        for (int n = 0; n < g->N; ++n)
+            for (size_t p = 0; p < P; ++p)
+                m = fmaxf(m, fabsf(conv_window_value(x, g, n, (int)(p / ow), (int)(p % ow), c, ky, kx)));
+        int eX = oracle_scale_exponent(m);
+        for (int n = 0; n < g->N; ++n)
+            for (size_t p = 0; p < P; ++p)
+                X[(size_t)n * P + p] = oracle_fixed_point(
+                    conv_window_value(x, g, n, (int)(p / ow), (int)(p % ow), c, ky, kx), eX, S);
+        for (int f = 0; f < g->F; ++f) t[f] = 0;
+        for (int n = 0; n < g->N; ++n)
+            for (int f = 0; f < g->F; ++f) {
+                const int* d = D + ((size_t)n * g->F + f) * P;
+                const int* xv = X + (size_t)n * P;
+                int64_t s = 0;
+                for (size_t p = 0; p < P; ++p) s += (int64_t)d[p] * xv[p];
+                t[f] += s;
+            }
+        for (int f = 0; f < g->F; ++f) dw[(size_t)f * K + k] = oracle_round_to_float(t[f], eF[f] + eX + e0);
+    }
+    free(eF); free(D); free(X); free(t);
+}
+
+/* Input gradient (repro_conv_cpu.h:72-91, repro_conv_math.cuh:132-157): dY quantised with one
+ * scale per image, all weights with one scale; dX[n][c][y][x] = round(sum over the windows
+ * covering the pixel and all filters of D * Wq, e_image + e_weights + e0). */
+void oracle_conv2d_grad_input(const float* dy, const float* w, float* dx, const oracle_conv_shape* g,
+                              int S) {
+    int oh = conv_oh(g), ow = conv_ow(g), e0 = -14 * (S - 1);
+    size_t per = (size_t)g->F * oh * ow, wn = (size_t)g->F * g->C * g->KH * g->KW;
+    int* eI = (int*)malloc(sizeof(int) * (size_t)g->N);
+    int* D = (int*)malloc(sizeof(int) * (size_t)g->N * per);
+    int* Wq = (int*)malloc(sizeof(int) * wn);
+    for (int n = 0; n < g->N; ++n) {
+        float m = 0.0f;
+        for (size_t i = 0; i < per; ++i) m = fmaxf(m, fabsf(dy[(size_t)n * per + i]));
+        eI[n] = oracle_scale_exponent(m);
+        for (size_t i = 0; i < per; ++i) D[(size_t)n * per + i] = oracle_fixed_point(dy[(size_t)n * per + i], eI[n], S);
+    }
+    float mw = 0.0f;
+    for (size_t i = 0; i < wn; ++i) mw = fmaxf(mw, fabsf(w[i]));
+    int eW = oracle_scale_exponent(mw);
+    for (size_t i = 0; i < wn; ++i) Wq[i] = oracle_fixed_point(w[i], eW, S);
+    for (int n = 0; n < g->N; ++n)
+        for (int c = 0; c < g->C; ++c)
+            for (int y = 0; y < g->H; ++y)
+                for (int xx = 0; xx < g->W; ++xx) {
+                    int64_t t = 0;
+                    for (int ky = 0; ky < g->KH; ++ky) {
+                        int ry = y + g->PY - ky;
+                        if (ry < 0 || ry % g->SY) continue;
+                        int oy = ry / g->SY;
+                        if (oy >= oh) continue;
+                        for (int kx = 0; kx < g->KW; ++kx) {
+                            int rx = xx + g->PX - kx;
+                            if (rx < 0 || rx % g->SX) continue;
+                            int ox = rx / g->SX;
+                            if (ox >= ow) continue;
+                            for (int f = 0; f < g->F; ++f)
+                                t += (int64_t)D[(((size_t)n * g->F + f) * oh + oy) * ow + ox] *
+                                     Wq[(((size_t)f * g->C + c) * g->KH + ky) * g->KW + kx];
+                        }
+                    }
+                    dx[(((size_t)n * g->C + c) * g->H + y) * g->W + xx] =
+                        oracle_round_to_float(t, eI[n] + eW + e0);
+                }
+    free(eI); free(D); free(Wq);
+}

@@ -31,6 +31,12 @@
  *                          overflow and non-finite inputs, sum and mean; oracle/_ref (the
  *                          reference's repro_sum_math.cuh compiled here).
  *   oracle_has_nonfinite   numpy.isfinite on the same arrays.
+ *   oracle_conv2d*         the five LeNet convolution hashes the reference records
+ *                          (gpt2_ops_suite/results/mac/cpu.txt:35-39); forward and weight
+ *                          gradient against oracle_cpu_gemm on the im2col matrix (an
+ *                          independent path); the input gradient against brute force with
+ *                          Python integers on small shapes; all three against oracle/_ref
+ *                          (the reference's repro_conv_cpu.h compiled here).
  */
 #ifndef REPRO_ORACLE_H
 #define REPRO_ORACLE_H
@@ -108,6 +114,20 @@ void oracle_splitmix64(uint64_t* out, size_t n, uint64_t seed);
 void oracle_exact_sum(const float* x, float* out, int A, int B, int C, int mean);
 /* 1 if x[0..n) holds a NaN or infinity (repro_torch/src/kernels.cu:10-14). */
 int oracle_has_nonfinite(const float* x, size_t n);
+
+/* Convolution geometry (repro_conv_cuda/repro_conv_math.cuh:29-42): input [N][C][H][W],
+ * weight [F][C][KH][KW], stride SY, SX, zero padding PY, PX. */
+typedef struct oracle_conv_shape {
+    int N, C, H, W, F, KH, KW, SY, SX, PY, PX;
+} oracle_conv_shape;
+/* out[N][F][OH][OW] (repro_conv_cuda/repro_conv_cpu.h:23-38). */
+void oracle_conv2d(const float* x, const float* w, float* out, const oracle_conv_shape* g, int S);
+/* dW[F][C][KH][KW] from dY[N][F][OH][OW] and x (repro_conv_cpu.h:40-70). */
+void oracle_conv2d_grad_weight(const float* dy, const float* x, float* dw,
+                               const oracle_conv_shape* g, int S);
+/* dX[N][C][H][W] from dY and the weights (repro_conv_cpu.h:72-91). */
+void oracle_conv2d_grad_input(const float* dy, const float* w, float* dx,
+                              const oracle_conv_shape* g, int S);
 
 /* FNV-1a 64 over raw bytes, chained from h (repro_gemm_cuda/repro_test_util.h:20-24). */
 uint64_t oracle_fnv1a64(const void* data, size_t n, uint64_t h);

@@ -15,7 +15,7 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared_symbols():
     names = set()
-    for header in ("repro_gemm.h", "repro_sum.h"):
+    for header in ("repro_gemm.h", "repro_sum.h", "repro_conv.h"):
         with open(os.path.join(REPO, "include", header)) as f:
             names |= set(re.findall(r"\b(rg_[a-z0-9_]+)\s*\(", f.read()))
     return sorted(names)
