@@ -15,12 +15,15 @@ from .repro_gemm import (  # noqa: F401
     Plan,
     ReproGemmError,
     algo_name,
+    bmm,
     gemm,
     make_plan,
+    make_plan_strided_batched,
     measure_mfma_int8_rate,
     plan_for_device,
     repro_gemm_fp32,
     repro_gemm_fp32_ws,
+    repro_gemm_strided_batched_fp32_ws,
     workspace_layout,
 )
 from .repro_sum import (  # noqa: F401

@@ -96,6 +96,15 @@ _SIGNATURES = {
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),
                                           ctypes.POINTER(rg_layout_info)]),
+    "rg_make_plan_strided_batched": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.c_int, ctypes.POINTER(rg_config),
+                                                    ctypes.POINTER(rg_plan)]),
+    "rg_gemm_strided_batched_fp32_ws": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.c_longlong, ctypes.c_longlong,
+        ctypes.c_void_p, ctypes.c_longlong, ctypes.c_longlong,
+        ctypes.c_void_p, ctypes.c_longlong, ctypes.c_longlong,
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(rg_config),
+        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rg_sum_config_init": (None, [ctypes.POINTER(rg_sum_config)]),
     "rg_make_sum_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(rg_sum_config), ctypes.POINTER(rg_sum_plan)]),

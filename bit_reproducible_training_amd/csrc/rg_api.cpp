@@ -61,11 +61,13 @@ void choose_chunks(int R, int K, bool strided, int* nch, int* kch) {
 }  // namespace
 
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
-                bool ta, bool tb, const DeviceInfo& dev, Layout* Lp, bool raw, bool gemm_bound) {
+                bool ta, bool tb, const DeviceInfo& dev, Layout* Lp, const PlanExtras& extras) {
     if (M <= 0 || N <= 0 || K <= 0 || split_k <= 0) return hipErrorInvalidValue;
     if (S < 1 || S > 3) return hipErrorInvalidValue;
+    const int batch = extras.batch;
+    if (batch < 1 || batch > 65535) return hipErrorInvalidValue;  // grid z
     const double d = max_fixed_point(S);
-    if (gemm_bound && (double)K * d * d > std::ldexp(1.0, 62)) return hipErrorInvalidValue;
+    if (extras.gemm_bound && (double)K * d * d > std::ldexp(1.0, 62)) return hipErrorInvalidValue;
     if (algo < RG_ALGO_AUTO || algo > RG_ALGO_TENSOR_CORE) return hipErrorInvalidValue;
 
     Layout L;
@@ -74,6 +76,7 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
     L.M = M;
     L.N = N;
     L.K = K;
+    L.batch = batch;
     L.ta = ta;
     L.tb = tb;
     L.a_strided = ta;   // A stored KxM: row r of op(A) is a column
@@ -85,6 +88,7 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
         L.Mp = round_up(M, PANEL_ROWS);
         L.Np = round_up(N, PANEL_ROWS);
         L.split = std::min(split_k, K);
+        if ((long long)L.split * batch > 65535) return hipErrorInvalidValue;  // grid z
         L.has_partial = true;
     } else {
         if (!dev.gfx950) return hipErrorNotSupported;
@@ -96,7 +100,7 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
             ti = tile_m / 64;
             tj = tile_n / 64;
         } else {
-            long long big = (long long)ceil_div(M, 128) * ceil_div(N, 128);
+            long long big = (long long)ceil_div(M, 128) * ceil_div(N, 128) * batch;
             if (big >= std::max(1, dev.num_cus / 2)) ti = tj = 2;
             else ti = tj = 1;
         }
@@ -111,7 +115,7 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
             // Default split: when the output tiles fill at most half of the GPU's block slots
             // (compute units x resident blocks, from the block's LDS ring), split K (int64
             // partials, summed exactly) up to the slot count, keeping >= 2 stages per part.
-            const long long tiles = (long long)(L.Mp / (64 * ti)) * (L.Np / (64 * tj));
+            const long long tiles = (long long)(L.Mp / (64 * ti)) * (L.Np / (64 * tj)) * batch;
             const int lds_bytes = 3 * (2 * ti + 2 * tj) * 2 * S * PANEL_BYTES;
             const int per_cu = std::max(1, std::min(2, (160 * 1024) / lds_bytes));
             const long long slots = (long long)std::max(1, dev.num_cus) * per_cu;
@@ -119,28 +123,31 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
                 split = std::max(split, (int)std::min<long long>(slots / tiles, std::max(1, nsteps / 2)));
         }
         L.split = std::min(split, nsteps);
-        L.has_partial = L.split > 1 || raw;
+        L.has_partial = L.split > 1 || extras.raw;
     }
 
-    choose_chunks(M, K, L.a_strided, &L.nch_a, &L.kch_a);
-    choose_chunks(N, K, L.b_strided, &L.nch_b, &L.kch_b);
+    const int rows_a = (int)std::min<long long>((long long)M * batch, 1 << 30);
+    const int rows_b = (int)std::min<long long>((long long)N * batch, 1 << 30);
+    choose_chunks(rows_a, K, L.a_strided, &L.nch_a, &L.kch_a);
+    choose_chunks(rows_b, K, L.b_strided, &L.nch_b, &L.kch_b);
 
     const size_t q_elem = L.algo == RG_ALGO_REFERENCE ? sizeof(int32_t) : (size_t)S;
+    const size_t Mt = (size_t)L.Mp * batch, Nt = (size_t)L.Np * batch;  // stacked rows
     size_t off = 0;
     L.qa = off;
-    off += align_up((size_t)L.Mp * L.Kp * q_elem);
+    off += align_up(Mt * L.Kp * q_elem);
     L.qb = off;
-    off += align_up((size_t)L.Np * L.Kp * q_elem);
+    off += align_up(Nt * L.Kp * q_elem);
     L.ea = off;
-    off += align_up((size_t)L.Mp * sizeof(int));
+    off += align_up(Mt * sizeof(int));
     L.eb = off;
-    off += align_up((size_t)L.Np * sizeof(int));
+    off += align_up(Nt * sizeof(int));
     L.pma = off;
-    off += align_up((size_t)L.nch_a * L.Mp * sizeof(float));
+    off += align_up((size_t)L.nch_a * Mt * sizeof(float));
     L.pmb = off;
-    off += align_up((size_t)L.nch_b * L.Np * sizeof(float));
+    off += align_up((size_t)L.nch_b * Nt * sizeof(float));
     L.part = off;
-    if (L.has_partial) off += align_up((size_t)L.split * M * N * sizeof(int64_t));
+    if (L.has_partial) off += align_up((size_t)batch * L.split * M * N * sizeof(int64_t));
     L.total = off;
     *Lp = L;
     return hipSuccess;
@@ -178,8 +185,8 @@ int query_device(DeviceInfo* info) {
     return hipSuccess;
 }
 
-int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L, bool raw,
-                              bool gemm_bound) {
+int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L,
+                              const PlanExtras& extras) {
     if (!cfg) return hipErrorInvalidValue;
     DeviceInfo dev{false, 0};
     if (cfg->algo != RG_ALGO_REFERENCE) {
@@ -187,11 +194,24 @@ int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout*
         if (e != hipSuccess) return e;
     }
     return plan_layout(M, N, K, cfg->split_k, cfg->tile_m, cfg->tile_n, cfg->algo, cfg->slices,
-                       cfg->trans_a != 0, cfg->trans_b != 0, dev, L, raw, gemm_bound);
+                       cfg->trans_a != 0, cfg->trans_b != 0, dev, L, extras);
+}
+
+GemmAddressing dense_addressing(const Layout& L) {
+    GemmAddressing a;
+    a.lda = L.ta ? L.M : L.K;
+    a.ldb = L.tb ? L.K : L.N;
+    a.ldc = L.N;
+    a.stride_a = (long long)L.M * L.K;
+    a.stride_b = (long long)L.K * L.N;
+    a.stride_c = (long long)L.M * L.N;
+    return a;
 }
 
 int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char* base,
-                hipStream_t stream, void* const* stage_events, const GemmOptions& opt) {
+                hipStream_t stream, void* const* stage_events, const GemmOptions& opt,
+                const GemmAddressing& addr) {
+    if ((opt.group_a > 0 || opt.group_b > 0) && L.batch != 1) return hipErrorInvalidValue;
     auto record = [&](int i) {
         if (stage_events) (void)hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream);
     };
@@ -204,16 +224,20 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     int64_t* part = L.has_partial ? reinterpret_cast<int64_t*>(base + L.part) : nullptr;
     const bool i32 = L.algo == RG_ALGO_REFERENCE;
 
-    auto desc = [&](const float* src, int R, int Rp, bool strided, int nch, int kch, float* pm,
-                    void* out, int* expo) {
+    auto desc = [&](const float* src, int R, int Rp, bool strided, long long ld, long long bstride,
+                    int nch, int kch, float* pm, void* out, int* expo) {
         SliceDesc d;
         d.src = src;
         d.R = R;
         d.K = L.K;
         d.Rp = Rp;
         d.Kp = L.Kp;
+        d.ld = ld;
+        d.batch = L.batch;
+        d.bstride = L.batch > 1 ? bstride : 0;
         d.strided = strided ? 1 : 0;
-        const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+        const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0 && ld % 4 == 0 &&
+                             d.bstride % 4 == 0;
         d.vec = aligned && (strided ? (R % 4 == 0) : (L.K % 4 == 0)) ? 1 : 0;
         d.nch = nch;
         d.kch = kch;
@@ -223,8 +247,11 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
         slice_grid(d);
         return d;
     };
-    const SliceDesc da = desc(A, L.M, L.Mp, L.a_strided, L.nch_a, L.kch_a, pma, qa, ea);
-    const SliceDesc db = desc(B, L.N, L.Np, L.b_strided, L.nch_b, L.kch_b, pmb, qb, eb);
+    const SliceDesc da = desc(A, L.M, L.Mp, L.a_strided, addr.lda, addr.stride_a, L.nch_a,
+                              L.kch_a, pma, qa, ea);
+    const SliceDesc db = desc(B, L.N, L.Np, L.b_strided, addr.ldb, addr.stride_b, L.nch_b,
+                              L.kch_b, pmb, qb, eb);
+    const OutAddr out{addr.ldc, addr.stride_c};
 
     record(0);
     launch_absmax(da, db, stream);
@@ -237,9 +264,9 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
                                   static_cast<const int32_t*>(qb), part, stream);
     else
         launch_contract_mfma(L, static_cast<const int8_t*>(qa), static_cast<const int8_t*>(qb),
-                             ea, eb, C, part, stream);
+                             ea, eb, C, out, part, stream);
     record(2);
-    if (L.has_partial && !opt.raw) launch_reduce_round(L, part, ea, eb, C, stream);
+    if (L.has_partial && !opt.raw) launch_reduce_round(L, part, ea, eb, C, out, stream);
     record(3);
     return hipGetLastError();
 }
@@ -326,7 +353,43 @@ int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int 
     if (e != hipSuccess) return e;
     if (!workspace || workspace_bytes < L.total) return hipErrorInvalidValue;
     return rg::gemm_launch(A, B, C, L, static_cast<char*>(workspace),
-                           static_cast<hipStream_t>(stream), stage_events, rg::GemmOptions());
+                           static_cast<hipStream_t>(stream), stage_events, rg::GemmOptions(),
+                           rg::dense_addressing(L));
+}
+
+int rg_make_plan_strided_batched(int M, int N, int K, int batch, const rg_config* cfg,
+                                 rg_plan* plan) {
+    if (!plan) return hipErrorInvalidValue;
+    rg::PlanExtras ex;
+    ex.batch = batch;
+    rg::Layout L;
+    int e = rg::layout_for_current_device(M, N, K, cfg, &L, ex);
+    if (e != hipSuccess) return e;
+    plan->algo = L.algo;
+    plan->split_k = L.split;
+    plan->workspace_bytes = L.total;
+    plan->tile_m = 64 * L.ti;
+    plan->tile_n = 64 * L.tj;
+    return hipSuccess;
+}
+
+int rg_gemm_strided_batched_fp32_ws(const float* A, long long lda, long long stride_a,
+                                    const float* B, long long ldb, long long stride_b, float* C,
+                                    long long ldc, long long stride_c, int M, int N, int K,
+                                    int batch, const rg_config* cfg, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+    if (!A || !B || !C || !cfg) return hipErrorInvalidValue;
+    rg::PlanExtras ex;
+    ex.batch = batch;
+    rg::Layout L;
+    int e = rg::layout_for_current_device(M, N, K, cfg, &L, ex);
+    if (e != hipSuccess) return e;
+    if (lda < (L.ta ? M : K) || ldb < (L.tb ? K : N) || ldc < N) return hipErrorInvalidValue;
+    if (stride_a < 0 || stride_b < 0 || stride_c < 0) return hipErrorInvalidValue;
+    if (!workspace || workspace_bytes < L.total) return hipErrorInvalidValue;
+    rg::GemmAddressing addr{lda, ldb, ldc, stride_a, stride_b, stride_c};
+    return rg::gemm_launch(A, B, C, L, static_cast<char*>(workspace),
+                           static_cast<hipStream_t>(stream), nullptr, rg::GemmOptions(), addr);
 }
 
 int rg_gemm_fp32(const float* A, const float* B, float* C, int M, int N, int K,

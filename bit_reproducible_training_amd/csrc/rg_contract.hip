@@ -35,7 +35,8 @@ template <int S, int WTI, int WTJ, int WGM, int WGN>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
               const int* __restrict__ eA, const int* __restrict__ eB, float* __restrict__ C,
-              int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n) {
+              int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n,
+              int Mp, int Np, long long ldc, long long c_item) {
 #if defined(__HIP_DEVICE_COMPILE__)  // buffer resources exist only in the device pass
     constexpr int L = 2 * S - 1;
     constexpr int NW = WGM * WGN;                  // wavefronts per block
@@ -55,6 +56,15 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     const int wm = wave / WGN, wn = wave % WGN;
     const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
     const int part = blockIdx.y;
+    // Item of a batch: its digit panels, exponents, output and partials follow the previous
+    // item's (blockIdx.z == 0 for a single GEMM).
+    const int item = blockIdx.z;
+    QA += (size_t)item * Mp * Kp * S;
+    QB += (size_t)item * Np * Kp * S;
+    eA += (size_t)item * Mp;
+    eB += (size_t)item * Np;
+    if (C != nullptr) C += (size_t)item * c_item;
+    if (partial != nullptr) partial += (size_t)item * split * M * N;
     const int nsteps = Kp / STEP_K;
     const int s0 = (int)((long long)nsteps * part / split);
     const int s1 = (int)((long long)nsteps * (part + 1) / split);
@@ -168,7 +178,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
                     for (int l = 0; l < L; ++l)
                         t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
                     if (partial == nullptr)
-                        C[(size_t)row * N + col] = round_to_float(t, eA[row] + ec);
+                        C[(size_t)row * ldc + col] = round_to_float(t, eA[row] + ec);
                     else
                         partial[((size_t)part * M + row) * N + col] = t;
                 }
@@ -184,70 +194,86 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 // this part's share of k. Always writes an int64 partial.
 __global__ void __launch_bounds__(256)
 contract_reference(const int32_t* __restrict__ X, const int32_t* __restrict__ Y,
-                   int64_t* __restrict__ partial, int M, int N, int K, int Kp, int split) {
+                   int64_t* __restrict__ partial, int M, int N, int K, int Kp, int split, int Mp,
+                   int Np) {
     const int c = blockIdx.x * 16 + (threadIdx.x & 15);
     const int r = blockIdx.y * 16 + (threadIdx.x >> 4);
-    const int part = blockIdx.z;
+    const int part = blockIdx.z % split, item = blockIdx.z / split;
     if (r >= M || c >= N) return;
     const int k0 = (int)((long long)K * part / split);
     const int k1 = (int)((long long)K * (part + 1) / split);
-    const int32_t* x = X + (size_t)r * Kp;
-    const int32_t* y = Y + (size_t)c * Kp;
+    const int32_t* x = X + ((size_t)item * Mp + r) * Kp;
+    const int32_t* y = Y + ((size_t)item * Np + c) * Kp;
     int64_t t = 0;
     for (int k = k0; k < k1; ++k) t += (int64_t)x[k] * y[k];
-    partial[((size_t)part * M + r) * N + c] = t;
+    partial[(((size_t)item * split + part) * M + r) * N + c] = t;
 }
 
-// Sums the split partials in int64 (order irrelevant: exact) and rounds once.
+// Sums the split partials in int64 (order irrelevant: exact) and rounds once; one thread per
+// output of every item.
 __global__ void __launch_bounds__(256)
 reduce_round(const int64_t* __restrict__ partial, const int* __restrict__ eA,
-             const int* __restrict__ eB, float* __restrict__ C, int M, int N, int split, int e0) {
+             const int* __restrict__ eB, float* __restrict__ C, int M, int N, int split, int e0,
+             int batch, int Mp, int Np, long long ldc, long long c_item) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t MN = (size_t)M * N;
-    if (idx >= MN) return;
-    const int r = (int)(idx / N), c = (int)(idx % N);
+    if (idx >= MN * batch) return;
+    const int item = (int)(idx / MN);
+    const size_t rc = idx - (size_t)item * MN;
+    const int r = (int)(rc / N), c = (int)(rc % N);
+    const int64_t* p0 = partial + (size_t)item * split * MN + rc;
     int64_t t = 0;
-    for (int p = 0; p < split; ++p) t += partial[(size_t)p * MN + idx];
-    C[idx] = round_to_float(t, eA[r] + eB[c] + e0);
+    for (int p = 0; p < split; ++p) t += p0[(size_t)p * MN];
+    C[(size_t)item * c_item + (size_t)r * ldc + c] =
+        round_to_float(t, eA[(size_t)item * Mp + r] + eB[(size_t)item * Np + c] + e0);
 }
 
 template <int S>
 static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
-                          const int* eb, float* C, int64_t* partial, hipStream_t stream) {
+                          const int* eb, float* C, OutAddr out, int64_t* partial,
+                          hipStream_t stream) {
     const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
-    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)L.split);
+    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)L.split, (unsigned)L.batch);
     // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64, 64x128, 64x64 = 4 wavefronts.
+#define RG_CONTRACT_ARGS qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n, L.Mp, L.Np, \
+                         out.ldc, out.c_item
     if (L.ti == 2 && L.tj == 2)
-        contract_mfma<S, 2, 1, 2, 4><<<grid, 512, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 2, 1, 2, 4><<<grid, 512, 0, stream>>>(RG_CONTRACT_ARGS);
     else if (L.ti == 2 && L.tj == 1)
-        contract_mfma<S, 2, 1, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 2, 1, 2, 2><<<grid, 256, 0, stream>>>(RG_CONTRACT_ARGS);
     else if (L.ti == 1 && L.tj == 2)
-        contract_mfma<S, 1, 2, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 1, 2, 2, 2><<<grid, 256, 0, stream>>>(RG_CONTRACT_ARGS);
     else
-        contract_mfma<S, 1, 1, 2, 2><<<grid, 256, 0, stream>>>(qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n);
+        contract_mfma<S, 1, 1, 2, 2><<<grid, 256, 0, stream>>>(RG_CONTRACT_ARGS);
+#undef RG_CONTRACT_ARGS
 }
 
 void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
-                          const int* eb, float* C, int64_t* partial, hipStream_t stream) {
+                          const int* eb, float* C, OutAddr out, int64_t* partial,
+                          hipStream_t stream) {
     switch (L.S) {
-        case 1: launch_mfma_s<1>(L, qa, qb, ea, eb, C, partial, stream); break;
-        case 2: launch_mfma_s<2>(L, qa, qb, ea, eb, C, partial, stream); break;
-        case 3: launch_mfma_s<3>(L, qa, qb, ea, eb, C, partial, stream); break;
+        case 1: launch_mfma_s<1>(L, qa, qb, ea, eb, C, out, partial, stream); break;
+        case 2: launch_mfma_s<2>(L, qa, qb, ea, eb, C, out, partial, stream); break;
+        case 3: launch_mfma_s<3>(L, qa, qb, ea, eb, C, out, partial, stream); break;
         default: break;
     }
 }
 
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,
                                int64_t* partial, hipStream_t stream) {
-    dim3 grid((unsigned)((L.N + 15) / 16), (unsigned)((L.M + 15) / 16), (unsigned)L.split);
-    contract_reference<<<grid, 256, 0, stream>>>(xa, xb, partial, L.M, L.N, L.K, L.Kp, L.split);
+    dim3 grid((unsigned)((L.N + 15) / 16), (unsigned)((L.M + 15) / 16),
+              (unsigned)(L.split * L.batch));
+    contract_reference<<<grid, 256, 0, stream>>>(xa, xb, partial, L.M, L.N, L.K, L.Kp, L.split,
+                                                 L.Mp, L.Np);
 }
 
 void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,
-                         float* C, hipStream_t stream) {
-    const size_t MN = (size_t)L.M * L.N;
-    unsigned blocks = (unsigned)((MN + 255) / 256);
-    reduce_round<<<blocks, 256, 0, stream>>>(partial, ea, eb, C, L.M, L.N, L.split, -14 * (L.S - 1));
+                         float* C, OutAddr out, hipStream_t stream) {
+    const size_t total = (size_t)L.M * L.N * L.batch;
+    unsigned blocks = (unsigned)((total + 255) / 256);
+    reduce_round<<<blocks, 256, 0, stream>>>(partial, ea, eb, C, L.M, L.N, L.split,
+                                             -14 * (L.S - 1), L.batch, L.Mp, L.Np, out.ldc,
+                                             out.c_item);
 }
 
 }  // namespace rg

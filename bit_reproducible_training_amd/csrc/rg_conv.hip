@@ -163,6 +163,14 @@ bool valid(const rg_conv_shape* s, int S) {
 
 enum class Kind { Forward, GradWeight, GradInput };
 
+// The convolution's GEMMs: its own int64 bound replaces the GEMM's; raw for the input gradient.
+PlanExtras conv_extras(bool raw) {
+    PlanExtras ex;
+    ex.raw = raw;
+    ex.gemm_bound = false;
+    return ex;
+}
+
 struct ConvPlan {
     Geom g;
     Layout L;        // the GEMM
@@ -184,18 +192,18 @@ int conv_plan(Kind kind, const rg_conv_shape* s, int S, ConvPlan* P) {
     switch (kind) {
         case Kind::Forward:       // C[W][F] = cols[W][K] * weight[F][K]^T
             cfg.trans_b = 1;
-            e = layout_for_current_device(W, g.F, g.K, &cfg, &p.L, false, false);
+            e = layout_for_current_device(W, g.F, g.K, &cfg, &p.L, conv_extras(false));
             b0 = (size_t)W * g.K * sizeof(float);   // cols
             b1 = (size_t)W * g.F * sizeof(float);   // Y rows
             break;
         case Kind::GradWeight:    // dW[F][K] = (dY rows[W][F])^T * cols[W][K]
             cfg.trans_a = 1;
-            e = layout_for_current_device(g.F, g.K, W, &cfg, &p.L, false, false);
+            e = layout_for_current_device(g.F, g.K, W, &cfg, &p.L, conv_extras(false));
             b0 = (size_t)W * g.F * sizeof(float);   // dY rows
             b1 = (size_t)W * g.K * sizeof(float);   // cols
             break;
         case Kind::GradInput:     // T[W][K] = dY rows[W][F] * weight[F][K], exact int64
-            e = layout_for_current_device(W, g.K, g.F, &cfg, &p.L, true, false);
+            e = layout_for_current_device(W, g.K, g.F, &cfg, &p.L, conv_extras(true));
             b0 = (size_t)W * g.F * sizeof(float);   // dY rows
             break;
     }
@@ -254,7 +262,8 @@ int rg_conv2d_ws(const float* x, const float* weight, float* out, const rg_conv_
     const size_t packed = (size_t)p.g.windows * p.g.K, outn = (size_t)p.g.windows * p.g.F;
     hipLaunchKernelGGL(rg::im2col_kernel, dim3((unsigned)rg::grid_for(packed)), dim3(rg::THREADS),
                        0, stream, x, cols, p.g);
-    e = rg::gemm_launch(cols, weight, yrows, p.L, base + p.gemm, stream, nullptr, rg::GemmOptions());
+    e = rg::gemm_launch(cols, weight, yrows, p.L, base + p.gemm, stream, nullptr, rg::GemmOptions(),
+                        rg::dense_addressing(p.L));
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rg::rows_to_nfp_kernel, dim3((unsigned)rg::grid_for(outn)),
                        dim3(rg::THREADS), 0, stream, yrows, out, p.g);
@@ -277,7 +286,8 @@ int rg_conv2d_grad_weight_ws(const float* dy, const float* x, float* dw, const r
                        dim3(rg::THREADS), 0, stream, dy, dyrows, p.g);
     hipLaunchKernelGGL(rg::im2col_kernel, dim3((unsigned)rg::grid_for(packed)), dim3(rg::THREADS),
                        0, stream, x, cols, p.g);
-    e = rg::gemm_launch(dyrows, cols, dw, p.L, base + p.gemm, stream, nullptr, rg::GemmOptions());
+    e = rg::gemm_launch(dyrows, cols, dw, p.L, base + p.gemm, stream, nullptr, rg::GemmOptions(),
+                        rg::dense_addressing(p.L));
     if (e != hipSuccess) return e;
     return hipGetLastError();
 }
@@ -301,7 +311,8 @@ int rg_conv2d_grad_input_ws(const float* dy, const float* weight, float* dx,
     opt.group_a = p.g.P;   // one scale per image
     opt.group_b = p.g.K;   // one scale for all weights
     opt.raw = true;
-    e = rg::gemm_launch(dyrows, weight, nullptr, p.L, gws, stream, nullptr, opt);
+    e = rg::gemm_launch(dyrows, weight, nullptr, p.L, gws, stream, nullptr, opt,
+                        rg::dense_addressing(p.L));
     if (e != hipSuccess) return e;
     const size_t pixels = (size_t)p.g.N * p.g.C * p.g.H * p.g.W;
     hipLaunchKernelGGL(rg::col2im_round_kernel, dim3((unsigned)rg::grid_for(pixels)),

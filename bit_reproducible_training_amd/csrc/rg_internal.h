@@ -20,10 +20,13 @@ constexpr int PANEL_K = 32;
 constexpr int PANEL_BYTES = 1024;
 constexpr int STEP_K = 64;  // k consumed per pipeline stage of the contraction
 
-// Where each region lives inside the caller's workspace, and how the work is split.
+// Where each region lives inside the caller's workspace, and how the work is split. A batch
+// of `batch` independent GEMMs of one shape stacks its items: item b's digit panels, exponents
+// and partial maxima follow item b-1's (per-item sizes Mp, Np), and its partials too.
 struct Layout {
     int algo;           // resolved RG_ALGO_* (never AUTO)
     int S, M, N, K;
+    int batch;          // items (1 for the plain GEMM)
     int Mp, Np, Kp;     // padded sizes: Mp, Np multiples of the block tile, Kp of STEP_K
     int ti, tj;         // MFMA block tile = (64*ti) x (64*tj); 0 for REFERENCE
     int split;          // split-K parts
@@ -44,26 +47,39 @@ struct DeviceInfo {
 // Architecture and compute-unit count of the current device (cached per device).
 int query_device(DeviceInfo* info);
 
-// Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported). raw: keep
-// the exact int64 sums T (the partial buffer [split][M][N], summed by the caller) instead of
-// rounding them to C. gemm_bound: apply the reference GEMM's K bound (K * max|X|^2 <= 2^62
-// with max|X| the largest digit-split value); callers with their own exactness bound (the
-// convolution's, on the clamped |X| <= 127*128^(S-1)) pass false.
-int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
-                bool ta, bool tb, const DeviceInfo& dev, Layout* L, bool raw = false,
-                bool gemm_bound = true);
+// Planner options beyond the reference's make_plan. raw: keep the exact int64 sums T (the
+// partial buffer [batch][split][M][N], summed by the caller) instead of rounding them to C.
+// gemm_bound: apply the reference GEMM's K bound (K * max|X|^2 <= 2^62 with max|X| the
+// largest digit-split value); callers with their own exactness bound (the convolution's, on
+// the clamped |X| <= 127*128^(S-1)) pass false. batch: independent GEMMs of one shape.
+struct PlanExtras {
+    bool raw = false;
+    bool gemm_bound = true;
+    int batch = 1;
+};
 
-// One operand of the slice split: op(X) has R rows of K values; `strided` when row r is
-// read along k with stride R (element (r, k) at src[k*R + r]), else src[r*K + k].
+// Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported).
+int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
+                bool ta, bool tb, const DeviceInfo& dev, Layout* L,
+                const PlanExtras& extras = PlanExtras());
+
+// One operand of the slice split: `batch` items, each op(X) of R rows of K values, item b at
+// src + b * bstride. Element (r, k) of an item is at [r * ld + k] (row access), or at
+// [k * ld + r] when `strided` (row r read along k with stride ld). Rows are stacked item by
+// item, each item padded to Rp rows: stacked row q = b * Rp + r indexes the partial maxima,
+// the exponents and the digit panels.
 struct SliceDesc {
     const float* src;
-    int R, K, Rp, Kp;
+    int R, K, Rp, Kp;   // per item
+    long long ld;       // elements between rows (row access) or between k (column access)
+    int batch;
+    long long bstride;  // elements between items
     int strided;
-    int vec;            // 16-byte vector loads allowed (alignment and K or R multiple of 4)
+    int vec;            // 16-byte vector loads allowed (alignment of src, ld, bstride; K or R % 4)
     int nch, kch;       // row-max chunks along K and their length
-    float* pmax;        // [nch][Rp] partial maxima
-    void* out;          // digit panels (or int32 [Rp][Kp] for the reference algorithm)
-    int* expo;          // [Rp] exponents
+    float* pmax;        // [nch][batch * Rp] partial maxima
+    void* out;          // digit panels (or int32 [batch * Rp][Kp] for the reference algorithm)
+    int* expo;          // [batch * Rp] exponents
     long long max_blocks, split_blocks;
 };
 
@@ -82,23 +98,39 @@ struct GemmOptions {
 
 // Layout for the current device (queried once per device and cached).
 int layout_for_current_device(int M, int N, int K, const rg_config* cfg, Layout* L,
-                              bool raw = false, bool gemm_bound = true);
+                              const PlanExtras& extras = PlanExtras());
 
-// The launch sequence of one GEMM on `stream` (slicing, contraction, final rounding unless
-// raw) into a workspace laid out by L at `base`. events: NULL or 4 hipEvent_t.
+// Operand and output addressing of a launch: leading dimensions and, for a batch, the element
+// strides between items. Plain row-major operands have lda = K (or M when transposed),
+// ldb = N (or K), ldc = N.
+struct GemmAddressing {
+    long long lda, ldb, ldc;
+    long long stride_a, stride_b, stride_c;
+};
+GemmAddressing dense_addressing(const Layout& L);
+
+// The launch sequence of L.batch GEMMs on `stream` (slicing, contraction, final rounding
+// unless raw) into a workspace laid out by L at `base`. events: NULL or 4 hipEvent_t.
 int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char* base,
-                hipStream_t stream, void* const* events, const GemmOptions& opt);
+                hipStream_t stream, void* const* events, const GemmOptions& opt,
+                const GemmAddressing& addr);
 
 // Kernel launchers (asynchronous on `stream`).
 void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream);
 void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream);
 // Replaces the partial row maxima of d by the maximum over each group of `group` rows.
 void launch_group_max(const SliceDesc& d, int group, hipStream_t stream);
+// Output addressing of the contraction and the final rounding: C of item b at
+// C + b * c_item, rows ldc apart.
+struct OutAddr {
+    long long ldc, c_item;
+};
 void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
-                          const int* eb, float* C, int64_t* partial, hipStream_t stream);
+                          const int* eb, float* C, OutAddr out, int64_t* partial,
+                          hipStream_t stream);
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,
                                int64_t* partial, hipStream_t stream);
 void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,
-                         float* C, hipStream_t stream);
+                         float* C, OutAddr out, hipStream_t stream);
 
 }  // namespace rg

@@ -32,19 +32,21 @@ __device__ __forceinline__ float max4(float4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
-// Row access, element (r, k) at src[r*K + k]: wavefront w of the operand handles row w / nch,
-// chunk w % nch.
+// Row access, element (r, k) of item b at src[b*bstride + r*ld + k]: wavefront w of the
+// operand handles row w / nch of all items' rows (item-major), chunk w % nch.
 __device__ void absmax_rows(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63;
     const long long w = blk * 4 + (threadIdx.x >> 6);
-    if (w >= (long long)d.R * d.nch) return;
-    const int r = (int)(w / d.nch), c = (int)(w % d.nch);
+    if (w >= (long long)d.batch * d.R * d.nch) return;
+    const long long i = w / d.nch;
+    const int c = (int)(w - i * d.nch);
+    const int b = (int)(i / d.R), r = (int)(i - (long long)b * d.R);
     const int k0 = c * d.kch;
     const int k1 = min(d.K, k0 + d.kch);
-    const float* row = d.src + (size_t)r * d.K;
+    const float* row = d.src + (size_t)b * d.bstride + (size_t)r * d.ld;
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
     int k = k0;
-    if (d.vec) {  // K % 4 == 0 and 16-byte aligned rows; kch is a multiple of 4
+    if (d.vec) {  // K % 4 == 0 and 16-byte aligned rows (src, ld, bstride); kch % 4 == 0
         const float4* p = reinterpret_cast<const float4*>(row);
         int q = k0 / 4 + lane;
         const int q1 = k1 / 4;
@@ -65,38 +67,42 @@ __device__ void absmax_rows(const SliceDesc& d, long long blk) {
         for (; k < k1; k += 64) m0 = fmaxf(m0, fabsf(row[k]));
     }
     float m = wave_max(fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-    if (lane == 0) d.pmax[(size_t)c * d.Rp + r] = m;
+    if (lane == 0) d.pmax[(size_t)c * d.batch * d.Rp + (size_t)b * d.Rp + r] = m;
 }
 
-// Column access, element (r, k) at src[k*R + r]: block g covers cols columns of chunk c;
-// its 4 wavefronts take every 4th k of the chunk and combine in LDS.
+// Column access, element (r, k) of item b at src[b*bstride + k*ld + r]: block (b, g, c)
+// covers cols columns of item b, chunk c; its 4 wavefronts take every 4th k of the chunk
+// and combine in LDS.
 __device__ void absmax_cols(const SliceDesc& d, long long blk) {
     __shared__ float4 part[4][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int cols = d.vec ? 256 : 64;
     const long long groups = (d.R + cols - 1) / cols;
-    if (blk >= groups * d.nch) return;
-    const int g = (int)(blk / d.nch), c = (int)(blk % d.nch);
+    if (blk >= (long long)d.batch * groups * d.nch) return;
+    const long long gi = blk / d.nch;
+    const int c = (int)(blk - gi * d.nch);
+    const int b = (int)(gi / groups), g = (int)(gi - (long long)b * groups);
+    const float* item = d.src + (size_t)b * d.bstride;
     const int k0 = c * d.kch;
     const int k1 = min(d.K, k0 + d.kch);
     float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (d.vec) {  // R % 4 == 0 and 16-byte aligned: lane owns columns 4*lane .. 4*lane+3
+    if (d.vec) {  // R, ld % 4 == 0 and 16-byte aligned: lane owns columns 4*lane .. 4*lane+3
         const int r = g * 256 + 4 * lane;
         if (r < d.R) {
-            const float* base = d.src + r;
+            const float* base = item + r;
             int k = k0 + wv;
             for (; k + 12 < k1; k += 16) {
-                float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.R);
-                float4 b = *reinterpret_cast<const float4*>(base + (size_t)(k + 4) * d.R);
-                float4 e = *reinterpret_cast<const float4*>(base + (size_t)(k + 8) * d.R);
-                float4 f = *reinterpret_cast<const float4*>(base + (size_t)(k + 12) * d.R);
+                float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.ld);
+                float4 b = *reinterpret_cast<const float4*>(base + (size_t)(k + 4) * d.ld);
+                float4 e = *reinterpret_cast<const float4*>(base + (size_t)(k + 8) * d.ld);
+                float4 f = *reinterpret_cast<const float4*>(base + (size_t)(k + 12) * d.ld);
                 m.x = fmaxf(m.x, fmaxf(fmaxf(fabsf(a.x), fabsf(b.x)), fmaxf(fabsf(e.x), fabsf(f.x))));
                 m.y = fmaxf(m.y, fmaxf(fmaxf(fabsf(a.y), fabsf(b.y)), fmaxf(fabsf(e.y), fabsf(f.y))));
                 m.z = fmaxf(m.z, fmaxf(fmaxf(fabsf(a.z), fabsf(b.z)), fmaxf(fabsf(e.z), fabsf(f.z))));
                 m.w = fmaxf(m.w, fmaxf(fmaxf(fabsf(a.w), fabsf(b.w)), fmaxf(fabsf(e.w), fabsf(f.w))));
             }
             for (; k < k1; k += 4) {
-                float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.R);
+                float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.ld);
                 m.x = fmaxf(m.x, fabsf(a.x));
                 m.y = fmaxf(m.y, fabsf(a.y));
                 m.z = fmaxf(m.z, fabsf(a.z));
@@ -106,15 +112,15 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
     } else {
         const int r = g * 64 + lane;
         if (r < d.R) {
-            const float* base = d.src + r;
+            const float* base = item + r;
             int k = k0 + wv;
             for (; k + 12 < k1; k += 16) {
-                m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.R]));
-                m.y = fmaxf(m.y, fabsf(base[(size_t)(k + 4) * d.R]));
-                m.z = fmaxf(m.z, fabsf(base[(size_t)(k + 8) * d.R]));
-                m.w = fmaxf(m.w, fabsf(base[(size_t)(k + 12) * d.R]));
+                m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.ld]));
+                m.y = fmaxf(m.y, fabsf(base[(size_t)(k + 4) * d.ld]));
+                m.z = fmaxf(m.z, fabsf(base[(size_t)(k + 8) * d.ld]));
+                m.w = fmaxf(m.w, fabsf(base[(size_t)(k + 12) * d.ld]));
             }
-            for (; k < k1; k += 4) m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.R]));
+            for (; k < k1; k += 4) m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.ld]));
             m.x = fmaxf(fmaxf(m.x, m.y), fmaxf(m.z, m.w));
         }
     }
@@ -130,7 +136,7 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
             t.z = fmaxf(t.z, u.z);
             t.w = fmaxf(t.w, u.w);
         }
-        float* out = d.pmax + (size_t)c * d.Rp;
+        float* out = d.pmax + (size_t)c * d.batch * d.Rp + (size_t)b * d.Rp;
         if (d.vec) {
             const int r = g * 256 + 4 * lane;
             if (r < d.R) *reinterpret_cast<float4*>(out + r) = t;  // Rp % 32 == 0: in range
@@ -190,12 +196,12 @@ __device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
 // or 16 int32 fixed-point values for INT32_OUT.
 template <int S, bool INT32_OUT>
 __device__ __forceinline__ void emit_panel(const SliceDesc& d, const float (&x)[16], const RowScale& rs,
-                                           int rp, int kp, int r, int h, int lane) {
+                                           int rp, int kp, int q, int h, int lane) {
     int X[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) X[j] = round_fixed(x[j], rs);
     if (INT32_OUT) {
-        int4* o = reinterpret_cast<int4*>(static_cast<int32_t*>(d.out) + (size_t)r * d.Kp + kp * PANEL_K + 16 * h);
+        int4* o = reinterpret_cast<int4*>(static_cast<int32_t*>(d.out) + (size_t)q * d.Kp + kp * PANEL_K + 16 * h);
 #pragma unroll
         for (int q = 0; q < 4; ++q) o[q] = make_int4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
         return;
@@ -220,21 +226,22 @@ __device__ __forceinline__ void emit_panel(const SliceDesc& d, const float (&x)[
                        pack4(dg[p][8], dg[p][9], dg[p][10], dg[p][11]), pack4(dg[p][12], dg[p][13], dg[p][14], dg[p][15]));
 }
 
-// The 16 values of lane (row r, half h) in panel kp; zero outside the matrix.
-__device__ __forceinline__ void load_panel(const SliceDesc& d, int kp, int r, int h, bool checked,
-                                           float (&x)[16]) {
+// The 16 values of lane (half h) of panel kp in the row whose element k = 0 is at rowp (null
+// for a padding row); zero outside the matrix.
+__device__ __forceinline__ void load_panel(const SliceDesc& d, int kp, const float* rowp, int h,
+                                           bool checked, float (&x)[16]) {
     const int k0 = kp * PANEL_K + 16 * h;
-    if (r >= d.R) {
+    if (rowp == nullptr) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) x[j] = 0.0f;
         return;
     }
     if (d.strided) {
-        const float* p = d.src + (size_t)k0 * d.R + r;
+        const float* p = rowp + (size_t)k0 * d.ld;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) x[j] = (!checked || k0 + j < d.K) ? p[(size_t)j * d.R] : 0.0f;
+        for (int j = 0; j < 16; ++j) x[j] = (!checked || k0 + j < d.K) ? p[(size_t)j * d.ld] : 0.0f;
     } else if (d.vec && (!checked || k0 + 16 <= d.K)) {
-        const float4* p = reinterpret_cast<const float4*>(d.src + (size_t)r * d.K + k0);
+        const float4* p = reinterpret_cast<const float4*>(rowp + k0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             float4 v = p[q];
@@ -244,7 +251,7 @@ __device__ __forceinline__ void load_panel(const SliceDesc& d, int kp, int r, in
             x[4 * q + 3] = v.w;
         }
     } else {
-        const float* p = d.src + (size_t)r * d.K + k0;
+        const float* p = rowp + k0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) x[j] = (!checked || k0 + j < d.K) ? p[j] : 0.0f;
     }
@@ -255,7 +262,7 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][32];
     __shared__ int sse[32];
     const int npk = d.Kp / PANEL_K;
-    const int rpanels = d.Rp / PANEL_ROWS;
+    const int rpanels = d.batch * (d.Rp / PANEL_ROWS);   // stacked over the items
     const int kgroups = (npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G);
     // Column access: neighbouring blocks take neighbouring row panels of the same k rows;
     // row access: neighbouring blocks continue along k of the same rows.
@@ -268,12 +275,16 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
         kg = (int)(blk % kgroups);
     }
     const int t = threadIdx.x;
+    // A panel never straddles two items (Rp is a multiple of the panel height).
+    const int item = (rp * PANEL_ROWS) / d.Rp;
+    const int r0 = rp * PANEL_ROWS - item * d.Rp;  // the panel's first row within its item
+    const size_t rows_total = (size_t)d.batch * d.Rp;
     {   // row maxima of this panel's 32 rows, reduced once for the whole block
         const int rr = t & 31, c0 = t >> 5;
-        const int row = rp * PANEL_ROWS + rr;
         float m = 0.0f;
-        if (row < d.R)
-            for (int c = c0; c < d.nch; c += 8) m = fmaxf(m, d.pmax[(size_t)c * d.Rp + row]);
+        if (r0 + rr < d.R)
+            for (int c = c0; c < d.nch; c += 8)
+                m = fmaxf(m, d.pmax[(size_t)c * rows_total + rp * PANEL_ROWS + rr]);
         smax[c0][rr] = m;
     }
     __syncthreads();
@@ -287,23 +298,27 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
     }
     __syncthreads();
     const int lane = t & 63, wv = t >> 6;
-    const int r = rp * PANEL_ROWS + (lane & 31), h = lane >> 5;
+    const int r = r0 + (lane & 31), h = lane >> 5;       // row within the item
+    const int q = rp * PANEL_ROWS + (lane & 31);         // stacked row
+    const float* rowp = r < d.R ? d.src + (size_t)item * d.bstride +
+                                      (d.strided ? (size_t)r : (size_t)r * d.ld)
+                                : nullptr;
     const RowScale rs = row_scale<S>(sse[lane & 31]);
     const int kpb = kg * 4 * SPLIT_G + wv * SPLIT_G;
     if (kpb + SPLIT_G <= npk && (kpb + SPLIT_G) * PANEL_K <= d.K) {
         // Every panel of this wavefront lies inside K: issue all loads, then round.
         float x[SPLIT_G][16];
 #pragma unroll
-        for (int g = 0; g < SPLIT_G; ++g) load_panel(d, kpb + g, r, h, false, x[g]);
+        for (int g = 0; g < SPLIT_G; ++g) load_panel(d, kpb + g, rowp, h, false, x[g]);
 #pragma unroll
-        for (int g = 0; g < SPLIT_G; ++g) emit_panel<S, INT32_OUT>(d, x[g], rs, rp, kpb + g, r, h, lane);
+        for (int g = 0; g < SPLIT_G; ++g) emit_panel<S, INT32_OUT>(d, x[g], rs, rp, kpb + g, q, h, lane);
     } else {
         for (int g = 0; g < SPLIT_G; ++g) {
             const int kp = kpb + g;
             if (kp >= npk) break;
             float x[16];
-            load_panel(d, kp, r, h, true, x);
-            emit_panel<S, INT32_OUT>(d, x, rs, rp, kp, r, h, lane);
+            load_panel(d, kp, rowp, h, true, x);
+            emit_panel<S, INT32_OUT>(d, x, rs, rp, kp, q, h, lane);
         }
     }
 }
@@ -319,12 +334,13 @@ __global__ void __launch_bounds__(256) split_kernel(SliceDesc a, SliceDesc b) {
 void slice_grid(SliceDesc& d) {
     if (d.strided) {
         const int cols = d.vec ? 256 : 64;
-        d.max_blocks = (long long)((d.R + cols - 1) / cols) * d.nch;
+        d.max_blocks = (long long)d.batch * ((d.R + cols - 1) / cols) * d.nch;
     } else {
-        d.max_blocks = ((long long)d.R * d.nch + 3) / 4;
+        d.max_blocks = ((long long)d.batch * d.R * d.nch + 3) / 4;
     }
     const int npk = d.Kp / PANEL_K;
-    d.split_blocks = (long long)(d.Rp / PANEL_ROWS) * ((npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G));
+    d.split_blocks = (long long)d.batch * (d.Rp / PANEL_ROWS) *
+                     ((npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G));
 }
 
 // Group scales: every row of each group of `group` consecutive rows gets the group's largest

@@ -2,7 +2,9 @@
 
 Names, fields and error behaviour follow repro_gemm_cuda/repro_gemm.cuh:25-75 (Algo,
 Config, Plan, make_plan, repro_gemm_fp32_ws, repro_gemm_fp32, algo_name) and the
-PyTorch binding repro_torch/src/bindings.cpp:43-66 (gemm). Everything runs through the
+PyTorch binding repro_torch/src/bindings.cpp:43-66 (gemm). The strided-batched form (bmm,
+repro_gemm_strided_batched_fp32_ws) has no counterpart in the reference, which lists batched
+GEMM for attention as still needed (README.md:29). Everything runs through the
 C ABI of librepro_gemm.so on the GPU; there is no CPU path. Device memory and streams
 come from PyTorch (torch.cuda = HIP on ROCm).
 """
@@ -114,6 +116,27 @@ def repro_gemm_fp32(A, B, C, M, N, K, cfg=None, stream=None):
     return lib.rg_gemm_fp32(A, B, C, int(M), int(N), int(K), ctypes.byref(c), stream)
 
 
+def make_plan_strided_batched(M, N, K, batch, cfg=None):
+    """Plan of `batch` independent GEMMs of one shape on the current device."""
+    cfg = cfg or Config()
+    c = cfg.to_c()
+    p = _lib.rg_plan()
+    _check(lib.rg_make_plan_strided_batched(int(M), int(N), int(K), int(batch), ctypes.byref(c),
+                                            ctypes.byref(p)), "make_plan_strided_batched")
+    return Plan(Algo(p.algo), p.split_k, p.workspace_bytes, p.tile_m, p.tile_n)
+
+
+def repro_gemm_strided_batched_fp32_ws(A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c,
+                                       M, N, K, batch, cfg, workspace, workspace_bytes,
+                                       stream=None):
+    """Raw-pointer strided-batched entry point (include/repro_gemm.h). Returns the code."""
+    c = cfg.to_c()
+    return lib.rg_gemm_strided_batched_fp32_ws(A, int(lda), int(stride_a), B, int(ldb),
+                                               int(stride_b), C, int(ldc), int(stride_c), int(M),
+                                               int(N), int(K), int(batch), ctypes.byref(c),
+                                               workspace, int(workspace_bytes), stream)
+
+
 def measure_mfma_int8_rate(dense=True):
     """Sustained int8 MFMA TOP/s of the current device with register operands (dense random
     bytes or zeros); the practical ceiling of the contraction under the power limit."""
@@ -171,4 +194,50 @@ def gemm(A, B, M, N, K, ta=False, tb=False, S=3, cfg=None, out=None):
     code = repro_gemm_fp32_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, cfg,
                               ws.data_ptr(), ws.numel(), stream)
     _check(code, "gemm")
+    return C
+
+
+def bmm(A, B, ta=False, tb=False, S=3, cfg=None, out=None):
+    """C[b] = op(A[b]) op(B[b]) for 3-D float32 GPU tensors, each item bit-identical to gemm()
+    on that item alone (its own row and column scales); on the current stream.
+
+    A is [batch, M, K] ([batch, K, M] if ta) and B is [batch, K, N] ([batch, N, K] if tb). They
+    may be strided views whose last dimension is contiguous (for example one attention head per
+    item of a [T, H * D] activation): the library reads them in place through leading
+    dimensions and batch strides. A batch dimension of size 1 broadcasts. C is [batch, M, N].
+    """
+    import torch
+
+    if A.dim() != 3 or B.dim() != 3:
+        raise ValueError("bmm: A and B must be 3-D")
+    if A.dtype != torch.float32 or B.dtype != torch.float32:
+        raise ValueError("bmm: A and B must be float32")
+    if not (A.is_cuda and B.is_cuda):
+        raise ValueError("bmm: A and B must be GPU tensors (no CPU path in this library)")
+    if A.stride(2) != 1:
+        A = A.contiguous()
+    if B.stride(2) != 1:
+        B = B.contiguous()
+    batch = max(A.shape[0], B.shape[0])
+    if A.shape[0] not in (1, batch) or B.shape[0] not in (1, batch):
+        raise ValueError("bmm: batch sizes differ")
+    M, K = (A.shape[2], A.shape[1]) if ta else (A.shape[1], A.shape[2])
+    Kb, N = (B.shape[2], B.shape[1]) if tb else (B.shape[1], B.shape[2])
+    if Kb != K:
+        raise ValueError("bmm: shape mismatch")
+    stride_a = A.stride(0) if A.shape[0] > 1 else 0
+    stride_b = B.stride(0) if B.shape[0] > 1 else 0
+    if cfg is None:
+        cfg = Config(slices=S, trans_a=bool(ta), trans_b=bool(tb))
+    plan = make_plan_strided_batched(M, N, K, batch, cfg)
+    C = out if out is not None else torch.empty((batch, M, N), dtype=torch.float32, device=A.device)
+    if C.shape != (batch, M, N) or C.stride(2) != 1:
+        raise ValueError("bmm: out must be [batch, M, N] with a contiguous last dimension")
+    ws = _workspace(torch, plan.workspace_bytes, A.device)
+    stream = torch.cuda.current_stream(A.device).cuda_stream
+    code = repro_gemm_strided_batched_fp32_ws(A.data_ptr(), A.stride(1), stride_a, B.data_ptr(),
+                                              B.stride(1), stride_b, C.data_ptr(), C.stride(1),
+                                              C.stride(0), M, N, K, batch, cfg, ws.data_ptr(),
+                                              ws.numel(), stream)
+    _check(code, "bmm")
     return C

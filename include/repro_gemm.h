@@ -116,6 +116,23 @@ int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_inf
 int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
                        rg_plan* plan, rg_layout_info* info);
 
+/* Strided-batched GEMM, no counterpart in the reference (which lists it as still needed for
+ * attention: README.md:29, repro_gemm_cuda/README.md:106). batch independent GEMMs
+ *   C_b[M,N] = op(A_b) op(B_b),  A_b = A + b*stride_a, B_b = B + b*stride_b, C_b = C + b*stride_c
+ * with leading dimensions (elements between rows of the stored matrices): A_b is MxK with
+ * row stride lda (KxM if trans_a), B_b is KxN with row stride ldb (NxK if trans_b), C_b is MxN
+ * with row stride ldc. Every item is bit-identical to rg_gemm_fp32_ws on that item alone
+ * (its own row and column scales). Items of C must not overlap. 1 (invalid value) as
+ * rg_make_plan, plus batch outside 1..65535, lda < (trans_a ? M : K), ldb < (trans_b ? K : N),
+ * ldc < N, or a negative stride. Asynchronous, allocation-free. */
+int rg_make_plan_strided_batched(int M, int N, int K, int batch, const rg_config* cfg,
+                                 rg_plan* plan);
+int rg_gemm_strided_batched_fp32_ws(const float* A, long long lda, long long stride_a,
+                                    const float* B, long long ldb, long long stride_b, float* C,
+                                    long long ldc, long long stride_c, int M, int N, int K,
+                                    int batch, const rg_config* cfg, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* Diagnostic, no counterpart in the reference: the sustained int8 MFMA rate of the current
  * (gfx950) device in TOP/s, measured with a kernel that keeps its operands in registers
  * (no memory traffic) for about a millisecond. dense = 1: random operand bytes, the
