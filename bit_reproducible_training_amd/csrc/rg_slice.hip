@@ -257,10 +257,53 @@ __device__ __forceinline__ void load_panel(const SliceDesc& d, int kp, const flo
     }
 }
 
+// Row access, one wavefront's SPLIT_G panels (32 rows x 32*SPLIT_G k) read through LDS: a
+// lane of the panel layout needs 16 consecutive k of one row, and loading that directly makes
+// every load instruction touch 32 rows 16 bytes at a time. Here instruction i loads whole
+// 512-byte row segments instead (lane L: row 2i + L/32, float4 L%32), the wavefront writes them
+// to its padded LDS tile and reads back in the panel layout. The row pitch of 132 floats puts
+// the 8 rows a ds_read_b128 phase reads in distinct banks.
+constexpr int STAGE_PITCH = 32 * SPLIT_G + 4;
+
+__device__ __forceinline__ void load_panels_staged(const SliceDesc& d, float* tile, int item, int r0,
+                                                   int kpb, int lane, float (&x)[SPLIT_G][16]) {
+    const int c4 = lane & 31;
+    float4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int row = 2 * i + (lane >> 5);
+        v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r0 + row < d.R)
+            v[i] = *reinterpret_cast<const float4*>(d.src + (size_t)item * d.bstride +
+                                                    (size_t)(r0 + row) * d.ld + kpb * PANEL_K + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        *reinterpret_cast<float4*>(tile + (2 * i + (lane >> 5)) * STAGE_PITCH + 4 * c4) = v[i];
+    // The tile is this wavefront's alone: order its LDS writes before the reads of other lanes.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* src = tile + (lane & 31) * STAGE_PITCH + 16 * (lane >> 5);
+#pragma unroll
+    for (int g = 0; g < SPLIT_G; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = *reinterpret_cast<const float4*>(src + g * PANEL_K + 4 * q);
+            x[g][4 * q + 0] = t.x;
+            x[g][4 * q + 1] = t.y;
+            x[g][4 * q + 2] = t.z;
+            x[g][4 * q + 3] = t.w;
+        }
+}
+
 template <int S, bool INT32_OUT>
 __device__ void split_operand(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][32];
     __shared__ int sse[32];
+    // Staging tiles of the row path, one per wavefront; allocated at launch (dynamic LDS) only
+    // when an operand of the launch takes that path, so column-access launches keep occupancy.
+    extern __shared__ float stage[];
     const int npk = d.Kp / PANEL_K;
     const int rpanels = d.batch * (d.Rp / PANEL_ROWS);   // stacked over the items
     const int kgroups = (npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G);
@@ -308,8 +351,13 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
     if (kpb + SPLIT_G <= npk && (kpb + SPLIT_G) * PANEL_K <= d.K) {
         // Every panel of this wavefront lies inside K: issue all loads, then round.
         float x[SPLIT_G][16];
+        if (!d.strided && d.vec) {
+            static_assert(SPLIT_G * PANEL_K == 128, "staged loads cover 2 rows x 128 k per instruction");
+            load_panels_staged(d, stage + wv * 32 * STAGE_PITCH, item, r0, kpb, lane, x);
+        } else {
 #pragma unroll
-        for (int g = 0; g < SPLIT_G; ++g) load_panel(d, kpb + g, rowp, h, false, x[g]);
+            for (int g = 0; g < SPLIT_G; ++g) load_panel(d, kpb + g, rowp, h, false, x[g]);
+        }
 #pragma unroll
         for (int g = 0; g < SPLIT_G; ++g) emit_panel<S, INT32_OUT>(d, x[g], rs, rp, kpb + g, q, h, lane);
     } else {
@@ -378,13 +426,15 @@ void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream) {
 
 void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream) {
     const unsigned blocks = (unsigned)(a.split_blocks + b.split_blocks);
+    const bool staged = (!a.strided && a.vec) || (!b.strided && b.vec);
+    const size_t lds = staged ? 4 * 32 * STAGE_PITCH * sizeof(float) : 0;
     switch (S * 2 + (int32_out ? 1 : 0)) {
-        case 2: split_kernel<1, false><<<blocks, 256, 0, stream>>>(a, b); break;
-        case 3: split_kernel<1, true><<<blocks, 256, 0, stream>>>(a, b); break;
-        case 4: split_kernel<2, false><<<blocks, 256, 0, stream>>>(a, b); break;
-        case 5: split_kernel<2, true><<<blocks, 256, 0, stream>>>(a, b); break;
-        case 6: split_kernel<3, false><<<blocks, 256, 0, stream>>>(a, b); break;
-        case 7: split_kernel<3, true><<<blocks, 256, 0, stream>>>(a, b); break;
+        case 2: split_kernel<1, false><<<blocks, 256, lds, stream>>>(a, b); break;
+        case 3: split_kernel<1, true><<<blocks, 256, lds, stream>>>(a, b); break;
+        case 4: split_kernel<2, false><<<blocks, 256, lds, stream>>>(a, b); break;
+        case 5: split_kernel<2, true><<<blocks, 256, lds, stream>>>(a, b); break;
+        case 6: split_kernel<3, false><<<blocks, 256, lds, stream>>>(a, b); break;
+        case 7: split_kernel<3, true><<<blocks, 256, lds, stream>>>(a, b); break;
         default: break;
     }
 }
