@@ -111,27 +111,71 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[i], RG_LDS_PTR(&slot[wave + NW * i][0]), 16, voff,
                                                      soff, 0, 0);
     };
+    // One stage: two k-steps of 32. Digits are read in the order a0 b0 a1 b1 ... and each
+    // digit product is issued as soon as both of its digits are in registers, with the reads
+    // of the next group already in flight, so a wavefront's first MFMA waits for three
+    // fragment reads rather than for the whole step (after the stage barrier, every
+    // wavefront of the CU reads at once). The scheduling-group barriers pin that order:
+    // DS read groups (mask 0x100) alternate with MFMA groups (mask 0x008).
     auto compute = [&](v4i (*slot)[64]) {
+        v4i a[2][S][WTI], b[2][S][WTJ];
+        auto load_a = [&](int kk, int p) {
+#pragma unroll
+            for (int ti = 0; ti < WTI; ++ti) a[kk][p][ti] = slot[((wm * WTI + ti) * 2 + kk) * S + p][lane];
+        };
+        auto load_b = [&](int kk, int q) {
+#pragma unroll
+            for (int tj = 0; tj < WTJ; ++tj) b[kk][q][tj] = slot[PA + ((wn * WTJ + tj) * 2 + kk) * S + q][lane];
+        };
+        auto mma = [&](int kk, int p, int q) {
+#pragma unroll
+            for (int ti = 0; ti < WTI; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < WTJ; ++tj)
+                    acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                        a[kk][p][ti], b[kk][q][tj], acc[p + q][ti][tj], 0, 0, 0);
+        };
+        constexpr int T = WTI * WTJ;  // MFMAs per digit product
+        // Reads that open a k-step: a0, b0 and (S > 1) a1.
+        auto open_step = [&](int kk) {
+            load_a(kk, 0);
+            load_b(kk, 0);
+            if (S > 1) load_a(kk, 1);
+        };
+        constexpr int OPEN = WTI + WTJ + (S > 1 ? WTI : 0);
+        open_step(0);
+        __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            v4i a[S][WTI], b[S][WTJ];
+            mma(kk, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
 #pragma unroll
-            for (int p = 0; p < S; ++p) {
+            for (int t = 1; t < S; ++t) {  // S <= 3: t is 1 or 2
+                // digit a_t is in: products (t, q < t); meanwhile read b_t
+                load_b(kk, t);
+                __builtin_amdgcn_sched_group_barrier(0x100, WTJ, 0);
 #pragma unroll
-                for (int ti = 0; ti < WTI; ++ti) a[p][ti] = slot[((wm * WTI + ti) * 2 + kk) * S + p][lane];
+                for (int q = 0; q < t; ++q) mma(kk, t, q);
+                if (t == 1) __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
+                else __builtin_amdgcn_sched_group_barrier(0x008, 2 * T, 0);
+                // digit b_t is in: products (p <= t, t); meanwhile read a_{t+1}, or open the
+                // next k-step
+                if (t + 1 < S) {
+                    load_a(kk, t + 1);
+                    __builtin_amdgcn_sched_group_barrier(0x100, WTI, 0);
+                } else if (kk == 0) {
+                    open_step(1);
+                    __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
+                }
 #pragma unroll
-                for (int tj = 0; tj < WTJ; ++tj) b[p][tj] = slot[PA + ((wn * WTJ + tj) * 2 + kk) * S + p][lane];
+                for (int p = 0; p <= t; ++p) mma(kk, p, t);
+                if (t == 1) __builtin_amdgcn_sched_group_barrier(0x008, 2 * T, 0);
+                else __builtin_amdgcn_sched_group_barrier(0x008, 3 * T, 0);
             }
-#pragma unroll
-            for (int p = 0; p < S; ++p)
-#pragma unroll
-                for (int q = 0; q < S; ++q)
-#pragma unroll
-                    for (int ti = 0; ti < WTI; ++ti)
-#pragma unroll
-                        for (int tj = 0; tj < WTJ; ++tj)
-                            acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                                a[p][ti], b[q][tj], acc[p + q][ti][tj], 0, 0, 0);
+            if (S == 1 && kk == 0) {
+                open_step(1);
+                __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
+            }
         }
     };
     // Stage s: wait for this wavefront's loads of stage s (stage s+1's may stay in flight),
