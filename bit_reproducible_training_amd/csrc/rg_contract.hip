@@ -29,6 +29,8 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 // s_waitcnt on vector-memory operations only: wait until at most n are outstanding.
 #define RG_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+// s_waitcnt on LDS (and scalar memory) operations only: wait until none is outstanding.
+#define RG_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8))
 #define RG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 template <int S, int WTI, int WTJ, int WGM, int WGN>
@@ -113,84 +115,101 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     };
     // One stage: two k-steps of 32. Digits are read in the order a0 b0 a1 b1 ... and each
     // digit product is issued as soon as both of its digits are in registers, with the reads
-    // of the next group already in flight, so a wavefront's first MFMA waits for three
-    // fragment reads rather than for the whole step (after the stage barrier, every
-    // wavefront of the CU reads at once). The scheduling-group barriers pin that order:
-    // DS read groups (mask 0x100) alternate with MFMA groups (mask 0x008).
-    auto compute = [&](v4i (*slot)[64]) {
-        v4i a[2][S][WTI], b[2][S][WTJ];
-        auto load_a = [&](int kk, int p) {
+    // of the next group already in flight, so a wavefront's first MFMA waits for a few
+    // fragment reads rather than for the whole step. The last product group of a stage
+    // (products (p, S-1) of its second k-step, operands already in registers) is issued
+    // after the next stage barrier, together with that stage's first reads: the MFMA pipe
+    // keeps working through the barrier and the reads' latency instead of draining. The
+    // scheduling-group barriers pin the order: DS read groups (mask 0x100) alternate with
+    // MFMA groups (mask 0x008).
+    v4i a[2][S][WTI], b[2][S][WTJ];
+    auto load_a = [&](v4i (*slot)[64], int kk, int p) {
 #pragma unroll
-            for (int ti = 0; ti < WTI; ++ti) a[kk][p][ti] = slot[((wm * WTI + ti) * 2 + kk) * S + p][lane];
-        };
-        auto load_b = [&](int kk, int q) {
+        for (int ti = 0; ti < WTI; ++ti) a[kk][p][ti] = slot[((wm * WTI + ti) * 2 + kk) * S + p][lane];
+    };
+    auto load_b = [&](v4i (*slot)[64], int kk, int q) {
 #pragma unroll
-            for (int tj = 0; tj < WTJ; ++tj) b[kk][q][tj] = slot[PA + ((wn * WTJ + tj) * 2 + kk) * S + q][lane];
-        };
-        auto mma = [&](int kk, int p, int q) {
+        for (int tj = 0; tj < WTJ; ++tj) b[kk][q][tj] = slot[PA + ((wn * WTJ + tj) * 2 + kk) * S + q][lane];
+    };
+    auto mma = [&](int kk, int p, int q) {
 #pragma unroll
-            for (int ti = 0; ti < WTI; ++ti)
+        for (int ti = 0; ti < WTI; ++ti)
 #pragma unroll
-                for (int tj = 0; tj < WTJ; ++tj)
-                    acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                        a[kk][p][ti], b[kk][q][tj], acc[p + q][ti][tj], 0, 0, 0);
-        };
-        constexpr int T = WTI * WTJ;  // MFMAs per digit product
-        // Reads that open a k-step: a0, b0 and (S > 1) a1.
-        auto open_step = [&](int kk) {
-            load_a(kk, 0);
-            load_b(kk, 0);
-            if (S > 1) load_a(kk, 1);
-        };
-        constexpr int OPEN = WTI + WTJ + (S > 1 ? WTI : 0);
-        open_step(0);
+            for (int tj = 0; tj < WTJ; ++tj)
+                acc[p + q][ti][tj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                    a[kk][p][ti], b[kk][q][tj], acc[p + q][ti][tj], 0, 0, 0);
+    };
+    constexpr int T = WTI * WTJ;  // MFMAs per digit product
+    constexpr int OPEN = WTI + WTJ + (S > 1 ? WTI : 0);
+    // Reads that open a k-step: a0, b0 and (S > 1) a1.
+    auto open_step = [&](v4i (*slot)[64], int kk) {
+        load_a(slot, kk, 0);
+        load_b(slot, kk, 0);
+        if (S > 1) load_a(slot, kk, 1);
+    };
+    // The deferred group of the previous stage: products (p, S-1) of its second k-step.
+    auto tail = [&]() {
+#pragma unroll
+        for (int p = 0; p < S; ++p) mma(1, p, S - 1);
+    };
+    auto compute = [&](v4i (*slot)[64], bool with_tail) {
+        open_step(slot, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
+        if (with_tail) {
+            tail();
+            if (S == 1) __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
+            else if (S == 2) __builtin_amdgcn_sched_group_barrier(0x008, 2 * T, 0);
+            else __builtin_amdgcn_sched_group_barrier(0x008, 3 * T, 0);
+        }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
+            if (S == 1 && kk == 1) break;  // its only product is the deferred group
             mma(kk, 0, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
+            if (S == 1) {
+                open_step(slot, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
+            }
 #pragma unroll
             for (int t = 1; t < S; ++t) {  // S <= 3: t is 1 or 2
                 // digit a_t is in: products (t, q < t); meanwhile read b_t
-                load_b(kk, t);
+                load_b(slot, kk, t);
                 __builtin_amdgcn_sched_group_barrier(0x100, WTJ, 0);
 #pragma unroll
                 for (int q = 0; q < t; ++q) mma(kk, t, q);
                 if (t == 1) __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
                 else __builtin_amdgcn_sched_group_barrier(0x008, 2 * T, 0);
                 // digit b_t is in: products (p <= t, t); meanwhile read a_{t+1}, or open the
-                // next k-step
+                // next k-step. The second k-step's last group is deferred (tail).
                 if (t + 1 < S) {
-                    load_a(kk, t + 1);
+                    load_a(slot, kk, t + 1);
                     __builtin_amdgcn_sched_group_barrier(0x100, WTI, 0);
                 } else if (kk == 0) {
-                    open_step(1);
+                    open_step(slot, 1);
                     __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
                 }
+                if (kk == 1 && t == S - 1) break;
 #pragma unroll
                 for (int p = 0; p <= t; ++p) mma(kk, p, t);
                 if (t == 1) __builtin_amdgcn_sched_group_barrier(0x008, 2 * T, 0);
                 else __builtin_amdgcn_sched_group_barrier(0x008, 3 * T, 0);
             }
-            if (S == 1 && kk == 0) {
-                open_step(1);
-                __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
-            }
         }
     };
-    // Stage s: wait for this wavefront's loads of stage s (stage s+1's may stay in flight),
-    // barrier (everyone's stage s has landed and everyone has finished stage s-1, whose slot
-    // is refilled next), issue stage s+2, contract stage s. Every LDS read of a stage feeds
-    // an MFMA issued before the next barrier, so no read can see the refill.
+    // Stage s: wait for this wavefront's loads of stage s (stage s+1's may stay in flight) and
+    // for its reads of stage s-1 (the deferred group's operands are in registers then),
+    // barrier (everyone's stage s has landed and everyone's reads of stage s-1 are done, so
+    // its slot can be refilled), issue stage s+2 into that slot, contract stage s.
     auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s) {
         if (s + 1 < s1) RG_WAIT_VMCNT(PW);
         else RG_WAIT_VMCNT(0);
+        RG_WAIT_LGKMCNT0();
         // The hardware barrier, plus a compiler barrier for LDS accesses (the s_barrier
         // intrinsic alone does not keep memory operations from moving across it, and
         // __syncthreads() would also wait for the loads still in flight into other slots).
         asm volatile("s_barrier" ::: "memory");
         if (s + 2 < s1) issue(refill, s + 2);
-        compute(cur);
+        compute(cur, s > s0);
     };
 
     if (s0 < s1) issue(lds[0], s0);
@@ -201,6 +220,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
         stage(lds[cur], lds[refill], s);
         cur = cur == 2 ? 0 : cur + 1;
     }
+    if (s0 < s1) tail();
 
     // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
     // column lane%32.
