@@ -22,7 +22,19 @@
 
 namespace rg {
 
-using repro_gemm::round_to_float;
+using repro_gemm::round_to_float_normal;
+
+// Zero, subnormal and overflowing results of the final rounding: rare, kept out of line so
+// the epilogue's common path stays short.
+__device__ __noinline__ float round_to_float_rare(int64_t T, int E) {
+    return repro_gemm::round_to_float(T, E);
+}
+
+__device__ __forceinline__ float round_output(int64_t T, int E) {
+    bool normal;
+    const float r = round_to_float_normal(T, E, &normal);
+    return normal ? r : round_to_float_rare(T, E);
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -242,7 +254,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
                     for (int l = 0; l < L; ++l)
                         t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
                     if (partial == nullptr)
-                        C[(size_t)row * ldc + col] = round_to_float(t, eA[row] + ec);
+                        C[(size_t)row * ldc + col] = round_output(t, eA[row] + ec);
                     else
                         partial[((size_t)part * M + row) * N + col] = t;
                 }
@@ -289,7 +301,7 @@ reduce_round(const int64_t* __restrict__ partial, const int* __restrict__ eA,
     int64_t t = 0;
     for (int p = 0; p < split; ++p) t += p0[(size_t)p * MN];
     C[(size_t)item * c_item + (size_t)r * ldc + c] =
-        round_to_float(t, eA[(size_t)item * Mp + r] + eB[(size_t)item * Np + c] + e0);
+        round_output(t, eA[(size_t)item * Mp + r] + eB[(size_t)item * Np + c] + e0);
 }
 
 template <int S>

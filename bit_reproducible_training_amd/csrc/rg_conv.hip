@@ -130,7 +130,7 @@ col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __re
                 for (int s = 0; s < split; ++s) t += part[(size_t)s * MN + at];
             }
         }
-        dx[i] = repro_gemm::round_to_float(t, ea[(size_t)n * g.P] + eW + e0);
+        dx[i] = repro_gemm::round_to_float_fast(t, ea[(size_t)n * g.P] + eW + e0);
     }
 }
 

@@ -110,4 +110,33 @@ RG_HD inline float round_to_float(int64_t T, int E) {
     return bits_to_float(sign | (uint32_t)(q << (ex + 149)));
 }
 
+// round_to_float(T, E) for the common case of a GEMM epilogue, without branches: when the
+// result's exponent before rounding is a normal one (*normal = true), q = the 24 leading bits
+// of |T| rounded to nearest-even and the float's bits are ((biased exponent - 1) << 23) + q,
+// where a rounding carry (q == 2^24) moves into the exponent field by itself and a carry out of
+// the largest binade gives exactly +-inf. Otherwise (zero, subnormal or out-of-range results)
+// *normal = false and the returned value is meaningless: use round_to_float.
+RG_HD inline float round_to_float_normal(int64_t T, int E, bool* normal) {
+    const uint64_t neg = (uint64_t)(T >> 63);           // all ones when T < 0
+    const uint64_t m = ((uint64_t)T ^ neg) - neg;       // |T|
+    const int p = 63 - clz64(m | 1);                    // leading bit of |T|
+    const int e = p + E + 127;                          // biased exponent before rounding
+    *normal = m != 0 && e >= 1 && e <= 254;
+    const int sh = p - 23;                              // bits below the 24-bit significand
+    const int down = sh > 0 ? sh : 0, up = sh < 0 ? -sh : 0;
+    const uint64_t top = m >> down;
+    const uint64_t rem = m & ((1ull << down) - 1);      // 0 when nothing is dropped
+    const uint64_t half = (1ull << down) >> 1;          // 0 when nothing is dropped
+    const uint32_t carry = (uint32_t)(down > 0) & (uint32_t)((rem > half) | ((rem == half) & (top & 1)));
+    const uint32_t q = ((uint32_t)top << up) + carry;
+    return bits_to_float((((uint32_t)(e - 1) << 23) + q) | ((uint32_t)neg & 0x80000000u));
+}
+
+// The same value as round_to_float(T, E) for every input; branch-free in the common case.
+RG_HD inline float round_to_float_fast(int64_t T, int E) {
+    bool normal;
+    const float r = round_to_float_normal(T, E, &normal);
+    return normal ? r : round_to_float(T, E);
+}
+
 }  // namespace repro_gemm
