@@ -58,6 +58,39 @@ void choose_chunks(int R, int K, bool strided, int* nch, int* kch) {
     *nch = ceil_div(K, *kch);
 }
 
+// Estimated contraction time (microseconds) of one block-tile / split choice, used only to
+// choose between plans (any choice gives the same bits). Blocks run in waves over the GPU's
+// block slots (compute units x blocks resident per compute unit, from the block's LDS ring);
+// a block costs a fixed prologue/epilogue plus one pipeline stage per 64 values of k of its
+// part; a split adds the int64 partials' traffic (written once, read once) at about 4 TB/s.
+// Constants are fitted to MI355X measurements of the 128x128 and 64x64 kernels at S = 3
+// (1.75 us per 128x128 stage, 1.0 us per 64x64 stage with two blocks per compute unit) and
+// scaled by the MFMA work per stage, S^2, for fewer slices.
+// Blocks of one MFMA tile resident per compute unit: the LDS ring (3 stages of the block's
+// digit panels) against 160 KiB, at most 2.
+int blocks_per_cu(int ti, int tj, int S) {
+    const int lds_bytes = 3 * (2 * ti + 2 * tj) * 2 * S * PANEL_BYTES;
+    return std::max(1, std::min(2, (160 * 1024) / lds_bytes));
+}
+
+double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split, int S,
+                 int num_cus, bool raw) {
+    const double tiles = (double)ceil_div(M, 64 * ti) * ceil_div(N, 64 * tj) * batch;
+    const int per_cu = blocks_per_cu(ti, tj, S);
+    const double slots = (double)std::max(1, num_cus) * per_cu;
+    const double waves = std::ceil(tiles * split / slots);
+    const double w = ti * tj / 4.0;  // work of a block stage relative to the 128x128 tile
+    const double stage_us = 0.2 + 1.55 * w * per_cu * (S * S / 9.0);
+    const double fixed_us = 2.0 + 8.0 * w * per_cu;
+    const double steps = std::ceil((double)nsteps / split);
+    double t = waves * (steps * stage_us + fixed_us);
+    if (split > 1 || raw) {
+        const double outs = (double)M * N * batch;
+        t += 3.0 + (8.0 * outs * (split + 1) + 4.0 * outs) / 4.0e6;
+    }
+    return t;
+}
+
 }  // namespace
 
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
@@ -93,35 +126,53 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
     } else {
         if (!dev.gfx950) return hipErrorNotSupported;
         L.algo = algo == RG_ALGO_TILED ? RG_ALGO_TILED : RG_ALGO_TENSOR_CORE;
-        int ti = 0, tj = 0;
+        const int nsteps = L.Kp / STEP_K;
+        const int min_split = ceil_div(nsteps, max_steps_per_part(S));
+        // Candidate block tiles: the forced one, or 128x128 and 64x64; candidate splits: the
+        // caller's (raised to the int32-exactness minimum), or, for the default split_k == 1,
+        // that minimum, the next 8 splits and the splits that exactly fill 1..16 waves of the
+        // GPU's block slots. The planner keeps the candidate with the lowest estimated time
+        // (plan_cost); ties keep the earlier candidate.
+        int tiles_cand[2][2];
+        int ntile = 0;
         if (algo == RG_ALGO_TILED) {
-            ti = tj = 1;
+            tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 1;
         } else if ((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128)) {
-            ti = tile_m / 64;
-            tj = tile_n / 64;
+            tiles_cand[ntile][0] = tile_m / 64; tiles_cand[ntile++][1] = tile_n / 64;
         } else {
-            long long big = (long long)ceil_div(M, 128) * ceil_div(N, 128) * batch;
-            if (big >= std::max(1, dev.num_cus / 2)) ti = tj = 2;
-            else ti = tj = 1;
+            tiles_cand[ntile][0] = 2; tiles_cand[ntile++][1] = 2;
+            tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 1;
+        }
+        const int split_lo = std::min(std::max(split_k, min_split), nsteps);
+        double best = -1.0;
+        int ti = 0, tj = 0, split = split_lo;
+        for (int c = 0; c < ntile; ++c) {
+            const int cti = tiles_cand[c][0], ctj = tiles_cand[c][1];
+            auto consider = [&](int sp) {
+                if (sp < split_lo || sp > nsteps) return;
+                const double t = plan_cost(M, N, nsteps, batch, cti, ctj, sp, S, dev.num_cus,
+                                           extras.raw);
+                if (best < 0.0 || t < best) {
+                    best = t;
+                    ti = cti;
+                    tj = ctj;
+                    split = sp;
+                }
+            };
+            consider(split_lo);
+            if (split_k != 1) continue;
+            for (int sp = split_lo + 1; sp <= split_lo + 8; ++sp) consider(sp);
+            const long long tiles = (long long)ceil_div(M, 64 * cti) * ceil_div(N, 64 * ctj) * batch;
+            const long long slots = (long long)std::max(1, dev.num_cus) * blocks_per_cu(cti, ctj, S);
+            for (int waves = 1; waves <= 16; ++waves) {
+                const long long sp = waves * slots / tiles;
+                if (sp > split_lo + 8 && sp <= nsteps) consider((int)sp);
+            }
         }
         L.ti = ti;
         L.tj = tj;
         L.Mp = round_up(M, 64 * ti);
         L.Np = round_up(N, 64 * tj);
-        const int nsteps = L.Kp / STEP_K;
-        const int min_split = ceil_div(nsteps, max_steps_per_part(S));
-        int split = std::max(split_k, min_split);
-        if (split_k == 1) {
-            // Default split: when the output tiles fill at most half of the GPU's block slots
-            // (compute units x resident blocks, from the block's LDS ring), split K (int64
-            // partials, summed exactly) up to the slot count, keeping >= 2 stages per part.
-            const long long tiles = (long long)(L.Mp / (64 * ti)) * (L.Np / (64 * tj)) * batch;
-            const int lds_bytes = 3 * (2 * ti + 2 * tj) * 2 * S * PANEL_BYTES;
-            const int per_cu = std::max(1, std::min(2, (160 * 1024) / lds_bytes));
-            const long long slots = (long long)std::max(1, dev.num_cus) * per_cu;
-            if (2 * tiles <= slots)
-                split = std::max(split, (int)std::min<long long>(slots / tiles, std::max(1, nsteps / 2)));
-        }
         L.split = std::min(split, nsteps);
         L.has_partial = L.split > 1 || extras.raw;
     }

@@ -119,23 +119,32 @@ def test_split_raised_for_exact_int32(S, limit):
     assert p.split_k == 3
 
 
-def test_default_split_fills_the_gpu():
-    """With the default split_k = 1, few output tiles get a K split (>= 2 stages per part);
-    an explicit split_k is honoured; one-stage K is never split."""
-    p, _ = _plan(1024, 64, 1024)          # 16 tiles of 64x64 (2 per CU), 16 stages of 64
-    assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 8)
-    p, _ = _plan(64, 64, 65536)           # 1 tile, 1024 stages: up to 512 block slots
-    assert p.split_k == 512
-    p, _ = _plan(1024, 768, 768)          # 192 tiles of 64x64 <= 512 / 2 slots
-    assert p.split_k == 2
-    p, _ = _plan(1024, 2304, 768)         # 144 tiles of 128x128 (1 per CU): more than half
+def test_default_plan_follows_the_cost_model():
+    """With the default split_k = 1 and tile hints, the planner picks the block tile and split
+    with the lowest estimated time: waves of blocks over the GPU's block slots times the
+    stages of a part, plus the int64 partials of a split. The cases below were measured on
+    MI355X, and the chosen plan was the fastest or within noise of it. An explicit split_k is
+    honoured; one-stage K is never split."""
+    p, _ = _plan(64, 64, 65536)           # 1 tile, 1024 stages: one wave of 512 parts
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 512)
+    p, _ = _plan(1024, 64, 1024)          # 16 tiles of 64x64, 16 stages: split to fill a wave
+    assert (p.tile_m, p.tile_n) == (64, 64) and p.split_k >= 8
+    p, _ = _plan(3072, 768, 8192, trans_a=True)   # 144 tiles of 128x128: split 3 = 432 blocks
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 3)
+    p, _ = _plan(1024, 1024, 65536)       # 64 tiles of 128x128, 1024 stages
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 4)
+    p, _ = _plan(8192, 768, 768, trans_b=True)    # 1536 tiles of 64x64 = 3 waves of 512
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 1)
+    p, _ = _plan(1024, 768, 768, trans_b=True)    # one wave either way: no split traffic
+    assert p.split_k == 1
+    p, _ = _plan(8192, 2304, 768, trans_b=True)   # 1152 tiles of 128x128
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
     p, _ = _plan(1024, 1024, 64)          # one stage only
     assert p.split_k == 1
     p, _ = _plan(1024, 64, 1024, split_k=2)
     assert p.split_k == 2
-    p, _ = _plan(4096, 4096, 4096)        # 1024 tiles of 128x128
-    assert p.split_k == 1
+    p, _ = _plan(4096, 4096, 4096)        # 1024 tiles of 128x128 = 4 full waves
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
 
 
 def test_split_clamped_to_k_steps():
