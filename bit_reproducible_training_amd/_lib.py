@@ -92,6 +92,9 @@ _SIGNATURES = {
                                            ctypes.POINTER(rg_config),
                                            ctypes.POINTER(rg_layout_info)]),
     "rg_measure_mfma_int8_rate": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+    "rg_test_round": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int,
+                                     ctypes.c_void_p]),
     "rg_plan_for_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),

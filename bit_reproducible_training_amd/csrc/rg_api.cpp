@@ -395,6 +395,17 @@ int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_inf
     return hipSuccess;
 }
 
+int rg_test_round(const int* levels, const long long* T, const int* E, float* out, long long n,
+                  int S, void* stream) {
+    if ((levels == nullptr) == (T == nullptr) || !E || !out || n < 0 || n > (1ll << 30))
+        return hipErrorInvalidValue;
+    if (levels && (S < 1 || S > 3)) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    rg::launch_test_round(levels, reinterpret_cast<const int64_t*>(T), E, out, n, S,
+                          static_cast<hipStream_t>(stream));
+    return hipGetLastError();
+}
+
 int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int K,
                     const rg_config* cfg, void* workspace, size_t workspace_bytes, void* stream,
                     void* const* stage_events) {

@@ -22,18 +22,56 @@
 
 namespace rg {
 
-using repro_gemm::round_to_float_normal;
-
-// Zero, subnormal and overflowing results of the final rounding: rare, kept out of line so
-// the epilogue's common path stays short.
+// round_to_float for the rare inputs the binary64 paths hand over (|T| near or above 2^53),
+// kept out of line so the epilogue's common path stays short.
 __device__ __noinline__ float round_to_float_rare(int64_t T, int E) {
     return repro_gemm::round_to_float(T, E);
 }
 
+// T = sum_l lv[l] * 2^(7 (L-1-l)) as an exact int64.
+template <int L>
+__device__ __forceinline__ int64_t combine_levels(const int (&lv)[L]) {
+    int64_t t = 0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) t += (int64_t)lv[l] * ((int64_t)1 << (7 * (L - 1 - l)));
+    return t;
+}
+
+// round_to_float(T, E) for T = combine_levels(lv), with the levels combined in binary64:
+// Horner steps h = 128 h + lv[l] over int32 levels stay below 2^53 in magnitude up to the
+// next-to-last level (|h| < 2^31 (1 + 2^7 + 2^14 + 2^21) < 2^53 for L = 5), so they are
+// exact; the last step is exact when the next-to-last |h| < 2^45 (then |T| < 2^52 + 2^31).
+// Scaling by 2^E is exact in binary64 when f64_scale_exact(E) (every exponent the slicing
+// produces is: |E| <= 2 * 149 + 28), and the conversion to binary32 is the one IEEE rounding
+// (nearest-even, subnormals, -0.0, overflow to infinity). *ok = false when a condition fails;
+// the value is then meaningless and round_to_float(combine_levels(lv), E) is the result.
+template <int L>
+__device__ __forceinline__ float round_levels_try(const int (&lv)[L], int E, bool* ok) {
+    double h = (double)lv[0];
+#pragma unroll
+    for (int l = 1; l + 1 < L; ++l) h = __builtin_fma(h, 128.0, (double)lv[l]);
+    bool exact = repro_gemm::f64_scale_exact(E);
+    if (L > 1) {
+        exact = exact && __builtin_fabs(h) < 0x1p45;
+        h = __builtin_fma(h, 128.0, (double)lv[L - 1]);
+    }
+    *ok = exact;
+    return (float)__builtin_ldexp(h, E);
+}
+
+template <int L>
+__device__ __forceinline__ float round_levels(const int (&lv)[L], int E) {
+    bool ok;
+    const float r = round_levels_try<L>(lv, E, &ok);
+    return __builtin_expect(ok, 1) ? r : round_to_float_rare(combine_levels<L>(lv), E);
+}
+
+// round_to_float(T, E) for an int64 T: repro_gemm::round_to_float_f64 with its rare
+// fallback out of line.
 __device__ __forceinline__ float round_output(int64_t T, int E) {
-    bool normal;
-    const float r = round_to_float_normal(T, E, &normal);
-    return normal ? r : round_to_float_rare(T, E);
+    bool ok;
+    const float r = repro_gemm::round_to_float_f64_try(T, E, &ok);
+    return __builtin_expect(ok, 1) ? r : round_to_float_rare(T, E);
 }
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -45,8 +83,18 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 #define RG_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8))
 #define RG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
+// Wavefronts per SIMD that the block tile's LDS ring allows (blocks per CU x wavefronts per
+// block / 4), capped at 2: the register budget the kernel is compiled for (at most 512 / that).
 template <int S, int WTI, int WTJ, int WGM, int WGN>
-__global__ void __launch_bounds__(64 * WGM * WGN)
+constexpr int contract_waves_per_simd() {
+    constexpr int lds = 3 * (WGM * WTI + WGN * WTJ) * 2 * S * PANEL_BYTES;
+    constexpr int blocks = (160 * 1024) / lds;
+    constexpr int w = blocks * WGM * WGN / 4;
+    return w < 1 ? 1 : (w > 2 ? 2 : w);
+}
+
+template <int S, int WTI, int WTJ, int WGM, int WGN>
+__global__ void __launch_bounds__(64 * WGM * WGN, (contract_waves_per_simd<S, WTI, WTJ, WGM, WGN>()))
 contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
               const int* __restrict__ eA, const int* __restrict__ eB, float* __restrict__ C,
               int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n,
@@ -235,32 +283,81 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     if (s0 < s1) tail();
 
     // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
-    // column lane%32.
+    // column lane%32. The exponent arrays cover the padded rows and columns, so their loads
+    // need no bounds check and are issued together before any arithmetic.
     const int e0 = -14 * (S - 1);
+    const int row0 = tm * BM + wm * WTI * 32 + 4 * (lane >> 5);
+    const bool rows_inside = tm * BM + BM <= M;  // uniform: no row of the block is past M
+    int col[WTJ];
 #pragma unroll
-    for (int ti = 0; ti < WTI; ++ti) {
+    for (int tj = 0; tj < WTJ; ++tj) col[tj] = tn * BN + (wn * WTJ + tj) * 32 + (lane & 31);
+    if (partial == nullptr) {
+        const bool inside = rows_inside && tn * BN + BN <= N;  // uniform: the whole block tile
+        int ec[WTJ];
 #pragma unroll
-        for (int tj = 0; tj < WTJ; ++tj) {
-            const int rbase = tm * BM + (wm * WTI + ti) * 32 + 4 * (lane >> 5);
-            const int col = tn * BN + (wn * WTJ + tj) * 32 + (lane & 31);
-            if (col < N) {
-                const int ec = eB[col] + e0;
+        for (int tj = 0; tj < WTJ; ++tj) ec[tj] = eB[col[tj]] + e0;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = rbase + 8 * (e >> 2) + (e & 3);
-                    if (row >= M) continue;
-                    int64_t t = 0;
+        for (int ti = 0; ti < WTI; ++ti) {
+            int er[16];
 #pragma unroll
-                    for (int l = 0; l < L; ++l)
-                        t += (int64_t)acc[l][ti][tj][e] * ((int64_t)1 << (7 * (L - 1 - l)));
-                    if (partial == nullptr)
-                        C[(size_t)row * ldc + col] = round_output(t, eA[row] + ec);
-                    else
-                        partial[((size_t)part * M + row) * N + col] = t;
+            for (int e = 0; e < 16; ++e) er[e] = eA[row0 + ti * 32 + 8 * (e >> 2) + (e & 3)];
+#pragma unroll
+            for (int tj = 0; tj < WTJ; ++tj) {
+                float* cp = C + (size_t)(row0 + ti * 32) * ldc + col[tj];
+                // Four rows at a time (registers e = 4q .. 4q+3: rows 8q .. 8q+3 of the lane's
+                // column), so few values are live at once.
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v[4];
+                    bool all_ok = true;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        int lv[L];
+#pragma unroll
+                        for (int l = 0; l < L; ++l) lv[l] = acc[l][ti][tj][4 * q + i];
+                        bool ok;
+                        v[i] = round_levels_try<L>(lv, er[4 * q + i] + ec[tj], &ok);
+                        all_ok = all_ok && ok;
+                    }
+                    if (__builtin_expect(!all_ok, 0)) {  // rare: these outputs exactly in int64
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            int lv[L];
+#pragma unroll
+                            for (int l = 0; l < L; ++l) lv[l] = acc[l][ti][tj][4 * q + i];
+                            v[i] = round_to_float_rare(combine_levels<L>(lv), er[4 * q + i] + ec[tj]);
+                        }
+                    }
+                    if (inside) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) cp[(size_t)(8 * q + i) * ldc] = v[i];
+                    } else if (col[tj] < N) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (rows_inside || row0 + ti * 32 + 8 * q + i < M) cp[(size_t)(8 * q + i) * ldc] = v[i];
+                    }
+                    // Keep the scheduler from hoisting every accumulator read to the top.
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            // Keep the scheduler from hoisting every accumulator read to the top.
-            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+#pragma unroll
+        for (int ti = 0; ti < WTI; ++ti) {
+#pragma unroll
+            for (int tj = 0; tj < WTJ; ++tj) {
+                if (col[tj] >= N) continue;
+                int64_t* pp = partial + ((size_t)part * M + row0 + ti * 32) * N + col[tj];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = 8 * (e >> 2) + (e & 3);
+                    int lv[L];
+#pragma unroll
+                    for (int l = 0; l < L; ++l) lv[l] = acc[l][ti][tj][e];
+                    if (rows_inside || row0 + ti * 32 + r < M) pp[(size_t)r * N] = combine_levels<L>(lv);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 #endif
@@ -302,6 +399,36 @@ reduce_round(const int64_t* __restrict__ partial, const int* __restrict__ eA,
     for (int p = 0; p < split; ++p) t += p0[(size_t)p * MN];
     C[(size_t)item * c_item + (size_t)r * ldc + c] =
         round_output(t, eA[(size_t)item * Mp + r] + eB[(size_t)item * Np + c] + e0);
+}
+
+// Test hooks: the epilogue roundings on arrays. levels: n x (2S-1) int32, most significant
+// level first.
+template <int L>
+__global__ void __launch_bounds__(256)
+round_levels_kernel(const int* __restrict__ lv, const int* __restrict__ E, float* __restrict__ out,
+                    long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    int v[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) v[l] = lv[i * L + l];
+    out[i] = round_levels<L>(v, E[i]);
+}
+
+__global__ void __launch_bounds__(256)
+round_output_kernel(const int64_t* __restrict__ T, const int* __restrict__ E,
+                    float* __restrict__ out, long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = round_output(T[i], E[i]);
+}
+
+void launch_test_round(const int* levels, const int64_t* T, const int* E, float* out, long long n,
+                       int S, hipStream_t stream) {
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    if (levels == nullptr) round_output_kernel<<<blocks, 256, 0, stream>>>(T, E, out, n);
+    else if (S == 1) round_levels_kernel<1><<<blocks, 256, 0, stream>>>(levels, E, out, n);
+    else if (S == 2) round_levels_kernel<3><<<blocks, 256, 0, stream>>>(levels, E, out, n);
+    else round_levels_kernel<5><<<blocks, 256, 0, stream>>>(levels, E, out, n);
 }
 
 template <int S>

@@ -132,5 +132,9 @@ void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t
                                int64_t* partial, hipStream_t stream);
 void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,
                          float* C, OutAddr out, hipStream_t stream);
+// The epilogue roundings on arrays (rg_test_round): levels != nullptr rounds n x (2S-1) int32
+// levels as the contraction's epilogue does, else n int64 values as reduce_round does.
+void launch_test_round(const int* levels, const int64_t* T, const int* E, float* out, long long n,
+                       int S, hipStream_t stream);
 
 }  // namespace rg

@@ -116,6 +116,16 @@ int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_inf
 int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
                        rg_plan* plan, rg_layout_info* info);
 
+/* Test hook, no counterpart in the reference: the GPU epilogue's final rounding on arrays,
+ * so tests can compare it with round_to_float on chosen inputs. Exactly one of levels and T
+ * is non-NULL. levels: n x (2S-1) int32 level sums per output, most significant first, rounded
+ * as the contraction's epilogue rounds T = sum_l levels[l] * 2^(7 (2S-2-l)); T: n int64
+ * values rounded as the split-K reduction does. out[i] = round_to_float(T_i, E[i]).
+ * Device pointers; asynchronous on stream; 1 (invalid value) for bad arguments or
+ * n > 2^30. */
+int rg_test_round(const int* levels, const long long* T, const int* E, float* out, long long n,
+                  int S, void* stream);
+
 /* Strided-batched GEMM, no counterpart in the reference (which lists it as still needed for
  * attention: README.md:29, repro_gemm_cuda/README.md:106). batch independent GEMMs
  *   C_b[M,N] = op(A_b) op(B_b),  A_b = A + b*stride_a, B_b = B + b*stride_b, C_b = C + b*stride_c

@@ -8,7 +8,9 @@
 // results do not depend on the floating-point environment (denormal flushing, FMA
 // contraction) of the compiler or the GPU. scale_exponent needs one correctly rounded
 // binary32 division; HIP's default (-fhip-fp32-correctly-rounded-divide-sqrt) and any
-// IEEE host compiler provide it. Do not build with -ffast-math or denormal flushing.
+// IEEE host compiler provide it. round_to_float_f64, the faster equivalent of round_to_float
+// used by the GPU epilogues, relies on exact binary64 arithmetic and one IEEE conversion to
+// binary32. Do not build with -ffast-math or denormal flushing.
 #include <cstdint>
 
 #if defined(__HIPCC__)
@@ -137,6 +139,31 @@ RG_HD inline float round_to_float_fast(int64_t T, int E) {
     bool normal;
     const float r = round_to_float_normal(T, E, &normal);
     return normal ? r : round_to_float(T, E);
+}
+
+// Exponents E for which T * 2^E is exact in binary64 for every |T| <= 2^53: no overflow
+// (2^53 * 2^E < 2^1024) and no underflow below the smallest normal (2^E >= 2^-1022).
+RG_HD inline bool f64_scale_exact(int E) { return (uint32_t)(E + 1022) <= 1022u + 970u; }
+
+// round_to_float(T, E) through binary64 when |T| <= 2^53: T is exact in a double (its two
+// 32-bit halves are, and hi * 2^32 + lo is representable, so the fused multiply-add does not
+// round), the scaling by 2^E is exact for f64_scale_exact(E), and the conversion to binary32
+// is the one rounding: nearest-even, with subnormal results, -0.0 for negative T that rounds
+// to zero and overflow to infinity, all by IEEE 754. Needs binary32 denormals (no flushing)
+// and the default rounding mode. Other inputs take round_to_float.
+// round_to_float_f64_try gives that value and *ok = true when -2^53 <= T < 2^53 and
+// f64_scale_exact(E); otherwise *ok = false and the returned value is meaningless.
+RG_HD inline float round_to_float_f64_try(int64_t T, int E, bool* ok) {
+    const int32_t hi = (int32_t)(T >> 32);
+    *ok = (uint32_t)(hi + (1 << 21)) < (1u << 22) && f64_scale_exact(E);
+    const double d = __builtin_fma((double)hi, 4294967296.0, (double)(uint32_t)T);
+    return (float)__builtin_ldexp(d, E);
+}
+
+RG_HD inline float round_to_float_f64(int64_t T, int E) {
+    bool ok;
+    const float r = round_to_float_f64_try(T, E, &ok);
+    return ok ? r : round_to_float(T, E);
 }
 
 }  // namespace repro_gemm

@@ -33,4 +33,8 @@ void hm_round_to_float_fast_n(const int64_t* T, const int* E, float* out, long l
     for (long long i = 0; i < n; ++i) out[i] = repro_gemm::round_to_float_fast(T[i], E[i]);
 }
 
+void hm_round_to_float_f64_n(const int64_t* T, const int* E, float* out, long long n) {
+    for (long long i = 0; i < n; ++i) out[i] = repro_gemm::round_to_float_f64(T[i], E[i]);
+}
+
 }  // extern "C"

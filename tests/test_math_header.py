@@ -29,6 +29,7 @@ def hm(tmp_path_factory):
     lib.hm_fixed_point_n.argtypes = [vp, vp, ctypes.c_int, vp, ll]
     lib.hm_round_to_float_n.argtypes = [vp, vp, vp, ll]
     lib.hm_round_to_float_fast_n.argtypes = [vp, vp, vp, ll]
+    lib.hm_round_to_float_f64_n.argtypes = [vp, vp, vp, ll]
     lib.hm_scale_exponent_count_range.argtypes = [ctypes.c_uint32, ctypes.c_uint32, vp]
     lib.hm_scale_exponent_count_range.restype = ll
     return lib
@@ -99,34 +100,38 @@ def test_round_to_float_vs_oracle(hm):
     assert np.array_equal(got.view(np.uint32), O.round_to_float_n(T, E).view(np.uint32))
 
 
-def _fast_vs_general(hm, T, E):
+def _fast_vs_general(hm, T, E, fn="hm_round_to_float_fast_n"):
     T = np.ascontiguousarray(T, np.int64)
     E = np.ascontiguousarray(E, np.int32)
     n = T.size
     fast = np.empty(n, np.float32)
     gen = np.empty(n, np.float32)
-    hm.hm_round_to_float_fast_n(T.ctypes.data, E.ctypes.data, fast.ctypes.data, n)
+    getattr(hm, fn)(T.ctypes.data, E.ctypes.data, fast.ctypes.data, n)
     hm.hm_round_to_float_n(T.ctypes.data, E.ctypes.data, gen.ctypes.data, n)
     return fast.view(np.uint32), gen.view(np.uint32)
 
 
-def test_round_to_float_fast_equals_general_and_oracle(hm):
-    """The branch-free epilogue rounding (round_to_float_fast) against round_to_float and the
-    oracle on every bit length of T and exponents across the whole range, including the
-    boundaries where it hands over to the general path (zero, subnormal, overflow)."""
+FAST = ["hm_round_to_float_fast_n", "hm_round_to_float_f64_n"]
+
+
+@pytest.mark.parametrize("fn", FAST)
+def test_round_to_float_fast_equals_general_and_oracle(hm, fn):
+    """The epilogue roundings (round_to_float_fast: branch-free integer; round_to_float_f64:
+    through binary64) against round_to_float and the oracle on every bit length of T and
+    exponents across the whole range, including the boundaries where they hand over to the
+    general path (zero, subnormal, overflow; |T| > 2^53 and exponents beyond binary64's)."""
     rng = np.random.default_rng(12)
     n = 3_000_000
     mag = rng.integers(0, 64, n)
     T = (rng.integers(0, 2 ** 63 - 1, n, dtype=np.int64) >> mag) * rng.choice([-1, 1], n)
     E = rng.integers(-340, 240, n).astype(np.int32)
-    fast, gen = _fast_vs_general(hm, T, E)
+    E[:1000] = rng.integers(-1200, 1100, 1000)
+    fast, gen = _fast_vs_general(hm, T, E, fn)
     assert np.array_equal(fast, gen)
     assert np.array_equal(fast, O.round_to_float_n(T, E).view(np.uint32))
 
 
-def test_round_to_float_fast_ties_and_binade_edges(hm):
-    """Exact ties (even and odd), one above/below a tie, carries into the next binade, the
-    carry out of the largest binade (+-inf), the smallest normal and the subnormal handover."""
+def _tie_cases():
     T, E = [], []
     rng = np.random.default_rng(13)
     for p in range(24, 63):
@@ -140,9 +145,22 @@ def test_round_to_float_fast_ties_and_binade_edges(hm):
                 for e_target in (-200, -150, -149, -127, -126, -125, -1, 0, 1, 100, 126, 127, 128):
                     T += [v, -v]
                     E += [e_target - p, e_target - p]
+    # around the binary64 handover: |T| = 2^53 +- small, and T = -2^53 exactly
+    for v in (2 ** 53 - 1, 2 ** 53, 2 ** 53 + 1, 2 ** 53 + 2, 2 ** 52 + 1, 2 ** 54 - 1):
+        for e in (-1100, -1023, -1022, -160, -100, 0, 70, 74, 75, 970, 971):
+            T += [v, -v]
+            E += [e, e]
     T += [0, 1, -1, 2 ** 62, -(2 ** 62), 2 ** 63 - 1, -(2 ** 63)]
     E += [0, -149, -150, 65, 65, 64, 64]
-    fast, gen = _fast_vs_general(hm, np.array(T, np.int64), np.array(E, np.int32))
+    return np.array(T, np.int64), np.array(E, np.int32)
+
+
+@pytest.mark.parametrize("fn", FAST)
+def test_round_to_float_fast_ties_and_binade_edges(hm, fn):
+    """Exact ties (even and odd), one above/below a tie, carries into the next binade, the
+    carry out of the largest binade (+-inf), the smallest normal and the subnormal handover,
+    and |T| around 2^53 with exponents at the edges of binary64's exact scaling."""
+    T, E = _tie_cases()
+    fast, gen = _fast_vs_general(hm, T, E, fn)
     assert np.array_equal(fast, gen)
-    assert np.array_equal(fast, O.round_to_float_n(np.array(T, np.int64),
-                                                   np.array(E, np.int32)).view(np.uint32))
+    assert np.array_equal(fast, O.round_to_float_n(T, E).view(np.uint32))
