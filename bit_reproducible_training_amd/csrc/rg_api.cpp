@@ -305,10 +305,29 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     const OutAddr out{addr.ldc, addr.stride_c};
 
     record(0);
-    launch_absmax(da, db, stream);
-    if (opt.group_a > 0) launch_group_max(da, opt.group_a, stream);
-    if (opt.group_b > 0) launch_group_max(db, opt.group_b, stream);
-    launch_split(da, db, L.S, i32, stream);
+    // Operands sliced in one pass; the others (and group scales, and the reference algorithm's
+    // int32 values) take the two passes.
+    const bool one_a = !i32 && opt.group_a == 0 && onepass_eligible(da);
+    const bool one_b = !i32 && opt.group_b == 0 && onepass_eligible(db);
+    if (one_a && one_b) {
+        launch_onepass(da, true, db, true, L.S, stream);
+    } else if (one_a != one_b) {
+        // one launch for the one-pass operand and the other's maxima, then the other's split
+        const SliceDesc& one = one_a ? da : db;
+        const SliceDesc& two = one_a ? db : da;
+        const int group = one_a ? opt.group_b : opt.group_a;
+        launch_onepass_absmax(one, two, L.S, stream);
+        if (group > 0) launch_group_max(two, group, stream);
+        SliceDesc none = one;
+        none.split_blocks = 0;
+        if (one_a) launch_split(none, two, L.S, i32, stream);
+        else launch_split(two, none, L.S, i32, stream);
+    } else {
+        launch_absmax(da, db, stream);
+        if (opt.group_a > 0) launch_group_max(da, opt.group_a, stream);
+        if (opt.group_b > 0) launch_group_max(db, opt.group_b, stream);
+        launch_split(da, db, L.S, i32, stream);
+    }
     record(1);
     if (i32)
         launch_contract_reference(L, static_cast<const int32_t*>(qa),

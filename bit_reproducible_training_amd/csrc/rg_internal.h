@@ -86,6 +86,19 @@ struct SliceDesc {
 // Fills max_blocks / split_blocks of d.
 void slice_grid(SliceDesc& d);
 
+// Single-pass slicing (row maxima, exponents and digit panels in one launch, each input read
+// once) of an operand that allows 16-byte loads, for padded K up to ONEPASS_MAX_K (row access)
+// or ONEPASS_MAX_K_COLUMNS (column access, whose 32-byte row segments fetch slower than the
+// two passes' wide ones at large K). launch_onepass slices the operands whose use_* is set
+// (both share K).
+constexpr int ONEPASS_MAX_K = 4096;
+constexpr int ONEPASS_MAX_K_COLUMNS = 3072;
+bool onepass_eligible(const SliceDesc& d);
+void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
+                    hipStream_t stream);
+// One launch: the one pass of `one` and the partial maxima of `two` (whose split follows).
+void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream);
+
 // Options of the launch sequence beyond the reference's GEMM, for the convolution's input
 // gradient: group_a > 0 gives every group of group_a consecutive rows of op(A) one scale (the
 // largest magnitude in the group; group_a >= M: one scale for all), likewise group_b for the

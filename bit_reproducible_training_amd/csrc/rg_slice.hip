@@ -34,9 +34,10 @@ __device__ __forceinline__ float max4(float4 v) {
 
 // Row access, element (r, k) of item b at src[b*bstride + r*ld + k]: wavefront w of the
 // operand handles row w / nch of all items' rows (item-major), chunk w % nch.
+template <int WAVES>
 __device__ void absmax_rows(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63;
-    const long long w = blk * 4 + (threadIdx.x >> 6);
+    const long long w = blk * WAVES + (threadIdx.x >> 6);
     if (w >= (long long)d.batch * d.R * d.nch) return;
     const long long i = w / d.nch;
     const int c = (int)(w - i * d.nch);
@@ -71,10 +72,11 @@ __device__ void absmax_rows(const SliceDesc& d, long long blk) {
 }
 
 // Column access, element (r, k) of item b at src[b*bstride + k*ld + r]: block (b, g, c)
-// covers cols columns of item b, chunk c; its 4 wavefronts take every 4th k of the chunk
-// and combine in LDS.
+// covers cols columns of item b, chunk c; its WAVES wavefronts take every WAVES-th k of the
+// chunk and combine in LDS.
+template <int WAVES>
 __device__ void absmax_cols(const SliceDesc& d, long long blk) {
-    __shared__ float4 part[4][64];
+    __shared__ float4 part[WAVES][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int cols = d.vec ? 256 : 64;
     const long long groups = (d.R + cols - 1) / cols;
@@ -91,17 +93,17 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
         if (r < d.R) {
             const float* base = item + r;
             int k = k0 + wv;
-            for (; k + 12 < k1; k += 16) {
+            for (; k + 3 * WAVES < k1; k += 4 * WAVES) {
                 float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.ld);
-                float4 b = *reinterpret_cast<const float4*>(base + (size_t)(k + 4) * d.ld);
-                float4 e = *reinterpret_cast<const float4*>(base + (size_t)(k + 8) * d.ld);
-                float4 f = *reinterpret_cast<const float4*>(base + (size_t)(k + 12) * d.ld);
+                float4 b = *reinterpret_cast<const float4*>(base + (size_t)(k + WAVES) * d.ld);
+                float4 e = *reinterpret_cast<const float4*>(base + (size_t)(k + 2 * WAVES) * d.ld);
+                float4 f = *reinterpret_cast<const float4*>(base + (size_t)(k + 3 * WAVES) * d.ld);
                 m.x = fmaxf(m.x, fmaxf(fmaxf(fabsf(a.x), fabsf(b.x)), fmaxf(fabsf(e.x), fabsf(f.x))));
                 m.y = fmaxf(m.y, fmaxf(fmaxf(fabsf(a.y), fabsf(b.y)), fmaxf(fabsf(e.y), fabsf(f.y))));
                 m.z = fmaxf(m.z, fmaxf(fmaxf(fabsf(a.z), fabsf(b.z)), fmaxf(fabsf(e.z), fabsf(f.z))));
                 m.w = fmaxf(m.w, fmaxf(fmaxf(fabsf(a.w), fabsf(b.w)), fmaxf(fabsf(e.w), fabsf(f.w))));
             }
-            for (; k < k1; k += 4) {
+            for (; k < k1; k += WAVES) {
                 float4 a = *reinterpret_cast<const float4*>(base + (size_t)k * d.ld);
                 m.x = fmaxf(m.x, fabsf(a.x));
                 m.y = fmaxf(m.y, fabsf(a.y));
@@ -114,13 +116,13 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
         if (r < d.R) {
             const float* base = item + r;
             int k = k0 + wv;
-            for (; k + 12 < k1; k += 16) {
+            for (; k + 3 * WAVES < k1; k += 4 * WAVES) {
                 m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.ld]));
-                m.y = fmaxf(m.y, fabsf(base[(size_t)(k + 4) * d.ld]));
-                m.z = fmaxf(m.z, fabsf(base[(size_t)(k + 8) * d.ld]));
-                m.w = fmaxf(m.w, fabsf(base[(size_t)(k + 12) * d.ld]));
+                m.y = fmaxf(m.y, fabsf(base[(size_t)(k + WAVES) * d.ld]));
+                m.z = fmaxf(m.z, fabsf(base[(size_t)(k + 2 * WAVES) * d.ld]));
+                m.w = fmaxf(m.w, fabsf(base[(size_t)(k + 3 * WAVES) * d.ld]));
             }
-            for (; k < k1; k += 4) m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.ld]));
+            for (; k < k1; k += WAVES) m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.ld]));
             m.x = fmaxf(fmaxf(m.x, m.y), fmaxf(m.z, m.w));
         }
     }
@@ -129,7 +131,7 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
     if (wv == 0) {
         float4 t = part[0][lane];
 #pragma unroll
-        for (int i = 1; i < 4; ++i) {
+        for (int i = 1; i < WAVES; ++i) {
             float4 u = part[i][lane];
             t.x = fmaxf(t.x, u.x);
             t.y = fmaxf(t.y, u.y);
@@ -150,9 +152,9 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
 __global__ void __launch_bounds__(256) absmax_kernel(SliceDesc a, SliceDesc b) {
     const long long blk = blockIdx.x;
     if (blk < a.max_blocks) {
-        if (a.strided) absmax_cols(a, blk); else absmax_rows(a, blk);
+        if (a.strided) absmax_cols<4>(a, blk); else absmax_rows<4>(a, blk);
     } else {
-        if (b.strided) absmax_cols(b, blk - a.max_blocks); else absmax_rows(b, blk - a.max_blocks);
+        if (b.strided) absmax_cols<4>(b, blk - a.max_blocks); else absmax_rows<4>(b, blk - a.max_blocks);
     }
 }
 
@@ -378,6 +380,216 @@ __global__ void __launch_bounds__(256) split_kernel(SliceDesc a, SliceDesc b) {
     else split_operand<S, INT32_OUT>(b, blk - a.split_blocks);
 }
 
+// One pass for padded K <= 256 * NF4 (both operands share K): block blk of an operand owns a
+// strip of 8 rows of op(X), a quarter of a 32-row panel, over all of K, held in registers (NF4
+// float4 per lane, so two blocks fit on a CU and one loads while the other rounds and
+// stores). Wavefront w covers k in [32*NF4*w, 32*NF4*(w+1)) for all 8 rows; instruction i
+// covers its k-panel i:
+//   row access    lane L loads row L/8, k = 4*(L%8)..+3 of the panel: 8 rows x 128 bytes;
+//   column access lane L loads k = L/2 of the panel, columns 4*(L%2)..+3: 32 k-rows x 32 bytes.
+// The rows' maxima are reduced with lane shuffles and across the 8 wavefronts in LDS, then each
+// lane rounds 4 values and writes their digits as one 4-byte word per digit plane: for row
+// access the lane's own values (four consecutive lanes fill a 16-byte run, eight rows a
+// 128-byte run); for column access after a transpose of the panel's 32 k x 8 columns through
+// the wavefront's LDS tile. Blocks blk, blk+8, blk+16, blk+24, which the dispatcher places on
+// the same XCD, take four neighbouring strips, so a column-access operand's 128-byte lines
+// (32 columns) are fetched into one L2 once.
+template <int S, int NF4>
+__device__ void slice_onepass(const SliceDesc& d, long long blk) {
+    __shared__ float smax[8][8];
+    __shared__ int sse[8];
+    __shared__ float tr[8][8][33];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int per_item = d.Rp / 8;
+    const long long nstrips = (long long)d.batch * per_item;
+    const long long st = (blk >> 5) * 32 + (blk & 7) * 4 + ((blk >> 3) & 3);
+    if (st >= nstrips) return;
+    const int item = (int)(st / per_item);
+    const int r0 = (int)(st - (long long)item * per_item) * 8;  // first row within the item
+    const int rp = (item * d.Rp + r0) / PANEL_ROWS;              // stacked 32-row panel
+    const int r_in = r0 & 24;                                    // strip offset in the panel
+    const float* base = d.src + (size_t)item * d.bstride;
+    const int kp0 = w * NF4;                                     // this wavefront's first k-panel
+    const int npk = d.Kp / PANEL_K;
+    float4 v[NF4];
+    if (!d.strided) {
+        const int row = r0 + (lane >> 3);
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NF4; ++i) {
+            const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
+            v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (row < d.R && k < d.K) v[i] = *reinterpret_cast<const float4*>(base + (size_t)row * d.ld + k);
+        }
+#pragma unroll
+        for (int i = 0; i < NF4; ++i) m = fmaxf(m, max4(v[i]));
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        if ((lane & 7) == 0) smax[w][lane >> 3] = m;
+    } else {
+        const int c = r0 + 4 * (lane & 1);
+        float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < NF4; ++i) {
+            const int k = (kp0 + i) * PANEL_K + (lane >> 1);
+            v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (k < d.K && c < d.R) v[i] = *reinterpret_cast<const float4*>(base + (size_t)k * d.ld + c);
+        }
+#pragma unroll
+        for (int i = 0; i < NF4; ++i) {
+            m.x = fmaxf(m.x, fabsf(v[i].x));
+            m.y = fmaxf(m.y, fabsf(v[i].y));
+            m.z = fmaxf(m.z, fabsf(v[i].z));
+            m.w = fmaxf(m.w, fabsf(v[i].w));
+        }
+#pragma unroll
+        for (int off = 2; off < 64; off <<= 1) {
+            m.x = fmaxf(m.x, __shfl_xor(m.x, off, 64));
+            m.y = fmaxf(m.y, __shfl_xor(m.y, off, 64));
+            m.z = fmaxf(m.z, __shfl_xor(m.z, off, 64));
+            m.w = fmaxf(m.w, __shfl_xor(m.w, off, 64));
+        }
+        if (lane < 2) {
+            smax[w][4 * lane + 0] = m.x;
+            smax[w][4 * lane + 1] = m.y;
+            smax[w][4 * lane + 2] = m.z;
+            smax[w][4 * lane + 3] = m.w;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        float m = smax[0][threadIdx.x];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) m = fmaxf(m, smax[i][threadIdx.x]);
+        const int se = scale_exponent(m);  // rows >= R have m == 0, so se == 0
+        sse[threadIdx.x] = se;
+        d.expo[(size_t)item * d.Rp + r0 + threadIdx.x] = se;
+    }
+    __syncthreads();
+    // Output word of lane (row or column ro of the strip, 16-k half h, word wd) in panel kp.
+    uint32_t* out = static_cast<uint32_t*>(d.out);
+    const int ro = lane >> 3, h = (lane >> 2) & 1, wd = lane & 3;
+    const RowScale rs = row_scale<S>(sse[ro]);
+    uint32_t* o0 = out + (size_t)rp * npk * S * (PANEL_BYTES / 4) + 4 * (r_in + ro + 32 * h) + wd;
+    float (*tile)[33] = tr[w];
+#pragma unroll
+    for (int i = 0; i < NF4; ++i) {
+        const int kp = kp0 + i;
+        if (kp >= npk) break;
+        float x[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        if (d.strided) {
+            // this lane's k-row lane/2, columns 4*(lane%2)..+3 -> tile[column][k-row]; then
+            // lane L takes column L/8, k = 4*(L%8)..+3
+            const int c4 = 4 * (lane & 1), kr = lane >> 1;
+            tile[c4 + 0][kr] = x[0];
+            tile[c4 + 1][kr] = x[1];
+            tile[c4 + 2][kr] = x[2];
+            tile[c4 + 3][kr] = x[3];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[j] = tile[ro][4 * (lane & 7) + j];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        int dg[S][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int X = round_fixed(x[j], rs);
+#pragma unroll
+            for (int p = S - 1; p >= 1; --p) {
+                dg[p][j] = (X << 25) >> 25;  // balanced digit in [-64, 63]
+                X = (X + 64) >> 7;
+            }
+            dg[0][j] = X;
+        }
+        uint32_t* o = o0 + (size_t)kp * S * (PANEL_BYTES / 4);
+#pragma unroll
+        for (int p = 0; p < S; ++p) o[p * (PANEL_BYTES / 4)] = pack4(dg[p][0], dg[p][1], dg[p][2], dg[p][3]);
+    }
+}
+
+template <int S, int NF4>
+__global__ void __launch_bounds__(512) slice_onepass_kernel(SliceDesc a, SliceDesc b, long long a_blocks) {
+    const long long blk = blockIdx.x;
+    if (blk < a_blocks) slice_onepass<S, NF4>(a, blk);
+    else slice_onepass<S, NF4>(b, blk - a_blocks);
+}
+
+// The one pass of operand `one` fused with the partial maxima (first of the two passes) of
+// operand `two`, so the two share the memory system instead of running one after the other.
+// The maxima use 8 wavefronts per block here (every 8th k of a chunk, or 8 rows).
+template <int S, int NF4>
+__global__ void __launch_bounds__(512) onepass_absmax_kernel(SliceDesc one, SliceDesc two, long long one_blocks) {
+    const long long blk = blockIdx.x;
+    if (blk < one_blocks) slice_onepass<S, NF4>(one, blk);
+    else if (two.strided) absmax_cols<8>(two, blk - one_blocks);
+    else absmax_rows<8>(two, blk - one_blocks);
+}
+
+// Blocks of the partial-maxima pass of d with 8 wavefronts per block.
+static long long absmax8_blocks(const SliceDesc& d) {
+    if (d.strided) return d.max_blocks;  // one block per (item, column group, chunk)
+    return ((long long)d.batch * d.R * d.nch + 7) / 8;
+}
+
+// Blocks of the one-pass slicing for one operand: its 8-row strips, rounded up to a multiple
+// of 32 so the XCD grouping of neighbouring strips stays inside the operand's blocks.
+static long long onepass_blocks(const SliceDesc& d) {
+    const long long strips = (long long)d.batch * (d.Rp / 8);
+    return (strips + 31) / 32 * 32;
+}
+
+bool onepass_eligible(const SliceDesc& d) {
+    return d.vec && d.Kp <= (d.strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K);
+}
+
+void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
+                    hipStream_t stream) {
+    const long long na = use_a ? onepass_blocks(a) : 0;
+    const long long nb = use_b ? onepass_blocks(b) : 0;
+    if (na + nb == 0) return;
+    const unsigned blocks = (unsigned)(na + nb);
+    const int kp = use_a ? a.Kp : b.Kp;
+    const int nf4 = kp <= 1024 ? 4 : (kp <= 2048 ? 8 : 16);
+#define RG_ONEPASS(SS, NF) slice_onepass_kernel<SS, NF><<<blocks, 512, 0, stream>>>(a, b, na)
+    switch (S * 100 + nf4) {
+        case 104: RG_ONEPASS(1, 4); break;
+        case 108: RG_ONEPASS(1, 8); break;
+        case 116: RG_ONEPASS(1, 16); break;
+        case 204: RG_ONEPASS(2, 4); break;
+        case 208: RG_ONEPASS(2, 8); break;
+        case 216: RG_ONEPASS(2, 16); break;
+        case 304: RG_ONEPASS(3, 4); break;
+        case 308: RG_ONEPASS(3, 8); break;
+        case 316: RG_ONEPASS(3, 16); break;
+        default: break;
+    }
+#undef RG_ONEPASS
+}
+
+void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream) {
+    const long long n1 = onepass_blocks(one);
+    const unsigned blocks = (unsigned)(n1 + absmax8_blocks(two));
+    const int nf4 = one.Kp <= 1024 ? 4 : (one.Kp <= 2048 ? 8 : 16);
+#define RG_FUSED(SS, NF) onepass_absmax_kernel<SS, NF><<<blocks, 512, 0, stream>>>(one, two, n1)
+    switch (S * 100 + nf4) {
+        case 104: RG_FUSED(1, 4); break;
+        case 108: RG_FUSED(1, 8); break;
+        case 116: RG_FUSED(1, 16); break;
+        case 204: RG_FUSED(2, 4); break;
+        case 208: RG_FUSED(2, 8); break;
+        case 216: RG_FUSED(2, 16); break;
+        case 304: RG_FUSED(3, 4); break;
+        case 308: RG_FUSED(3, 8); break;
+        case 316: RG_FUSED(3, 16); break;
+        default: break;
+    }
+#undef RG_FUSED
+}
+
 // Grid sizes of the two passes for one operand.
 void slice_grid(SliceDesc& d) {
     if (d.strided) {
@@ -426,7 +638,8 @@ void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream) {
 
 void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream) {
     const unsigned blocks = (unsigned)(a.split_blocks + b.split_blocks);
-    const bool staged = (!a.strided && a.vec) || (!b.strided && b.vec);
+    const bool staged = (a.split_blocks > 0 && !a.strided && a.vec) ||
+                        (b.split_blocks > 0 && !b.strided && b.vec);
     const size_t lds = staged ? 4 * 32 * STAGE_PITCH * sizeof(float) : 0;
     switch (S * 2 + (int32_out ? 1 : 0)) {
         case 2: split_kernel<1, false><<<blocks, 256, lds, stream>>>(a, b); break;

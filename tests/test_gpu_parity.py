@@ -145,6 +145,43 @@ def test_slicing_kernel_digits_and_exponents(torch_gpu, S, ta, tb):
         assert not e[Xo.shape[0]:].any()
 
 
+# Shapes that route the slicing through each of its paths: one pass for rows (16-byte loads,
+# padded K <= 4096) and columns (padded K <= 3072), the fused one-pass + maxima launch when
+# only one operand qualifies (with row or column maxima for the other), and two passes.
+SLICE_ROUTES = [(96, 68, 1000), (100, 64, 2052), (64, 100, 3076), (68, 96, 4100),
+                (96, 64, 1001), (97, 70, 1536), (128, 64, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SLICE_ROUTES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_slicing_routes_digits_exponents_and_result(torch_gpu, M, N, K, ta, tb):
+    """Digits, exponents and padding of both operands, and the GEMM's bits, against the
+    oracle on every route of the slicing (S = 3; S = 1 and 2 on the one-pass shapes)."""
+    torch = torch_gpu
+    rng = np.random.default_rng(M * 7 + N * 3 + K + ta * 2 + tb)
+    A = (rng.standard_normal(M * K) * 2.0 ** rng.integers(-20, 20, M * K)).astype(np.float32)
+    B = rng.standard_normal(N * K).astype(np.float32)
+    A[:K] = 0.0
+    for S in ((1, 2, 3) if K in (1000, 2052) else (3,)):
+        X, Y, eA, eB = O.quantize(A, B, M, N, K, ta, tb, S)
+        cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb)
+        note("slice route M=%d N=%d K=%d ta=%d tb=%d S=%d" % (M, N, K, ta, tb, S))
+        C, plan, ws = run(torch, A, B, M, N, K, cfg)
+        info = rg.workspace_layout(M, N, K, cfg)
+        w = ws.cpu().numpy()
+        for off, R, Xo, eo, eoff in ((info.qa, info.Mp, X, eA, info.ea), (info.qb, info.Np, Y, eB, info.eb)):
+            d, Xg = decode_digits(w, off, R, info.Kp, S)
+            assert np.abs(d[0]).max() <= 127
+            if S > 1:
+                assert d[1:].min() >= -64 and d[1:].max() <= 63
+            assert np.array_equal(Xg[:Xo.shape[0], :K], Xo)
+            assert not Xg[Xo.shape[0]:].any() and not Xg[:, K:].any()
+            e = w[eoff:eoff + 4 * R].view(np.int32)
+            assert np.array_equal(e[:Xo.shape[0]], eo)
+            assert not e[Xo.shape[0]:].any()
+        assert np.array_equal(bits(C), O.cpu_gemm(A, B, M, N, K, ta, tb, S).view(np.uint32))
+
+
 @pytest.mark.parametrize("split", [2, 3])
 def test_contraction_exact_products(torch_gpu, split):
     """Stage check of the contraction: the int64 split-K partials sum to the exact
