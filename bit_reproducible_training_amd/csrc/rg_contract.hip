@@ -178,10 +178,12 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // of the next group already in flight, so a wavefront's first MFMA waits for a few
     // fragment reads rather than for the whole step. The last product group of a stage
     // (products (p, S-1) of its second k-step, operands already in registers) is issued
-    // after the next stage barrier, together with that stage's first reads: the MFMA pipe
-    // keeps working through the barrier and the reads' latency instead of draining. The
-    // scheduling-group barriers pin the order: DS read groups (mask 0x100) alternate with
-    // MFMA groups (mask 0x008).
+    // after the next stage barrier, interleaved with that stage's first reads and its copy
+    // issue: deferred product (0, S-1), the opening reads, product (1, S-1), the copies into
+    // the freed slot, product (2, S-1). The matrix cores start right after the barrier and
+    // keep working through the reads' latency and the copy issue instead of draining. The
+    // scheduling-group barriers pin the order: DS read groups (mask 0x100), VMEM groups
+    // (0x020) and MFMA groups (0x008).
     v4i a[2][S][WTI], b[2][S][WTJ];
     auto load_a = [&](v4i (*slot)[64], int kk, int p) {
 #pragma unroll
@@ -212,14 +214,24 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #pragma unroll
         for (int p = 0; p < S; ++p) mma(1, p, S - 1);
     };
-    auto compute = [&](v4i (*slot)[64], bool with_tail) {
+    auto compute = [&](v4i (*slot)[64], bool with_tail, v4i (*refill)[64], int s_refill, bool do_issue) {
+        if (with_tail) {
+            mma(1, 0, S - 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
+        }
         open_step(slot, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, OPEN, 0);
-        if (with_tail) {
-            tail();
-            if (S == 1) __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
-            else if (S == 2) __builtin_amdgcn_sched_group_barrier(0x008, 2 * T, 0);
-            else __builtin_amdgcn_sched_group_barrier(0x008, 3 * T, 0);
+        if (with_tail && S > 1) {
+            mma(1, 1, S - 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
+        }
+        if (do_issue) {
+            issue(refill, s_refill);
+            __builtin_amdgcn_sched_group_barrier(0x020, PW, 0);
+        }
+        if (with_tail && S > 2) {
+            mma(1, 2, S - 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
@@ -259,8 +271,8 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // Stage s: wait for this wavefront's loads of stage s (stage s+1's may stay in flight) and
     // for its reads of stage s-1 (the deferred group's operands are in registers then),
     // barrier (everyone's stage s has landed and everyone's reads of stage s-1 are done, so
-    // its slot can be refilled), issue stage s+2 into that slot, contract stage s.
-    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s) {
+    // its slot can be refilled), contract stage s, issuing stage s+2 into that slot.
+    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s, bool do_issue, bool with_tail) {
         if (s + 1 < s1) RG_WAIT_VMCNT(PW);
         else RG_WAIT_VMCNT(0);
         RG_WAIT_LGKMCNT0();
@@ -268,18 +280,22 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
         // intrinsic alone does not keep memory operations from moving across it, and
         // __syncthreads() would also wait for the loads still in flight into other slots).
         asm volatile("s_barrier" ::: "memory");
-        if (s + 2 < s1) issue(refill, s + 2);
-        compute(cur, s > s0);
+        compute(cur, with_tail, refill, s + 2, do_issue);
     };
 
     if (s0 < s1) issue(lds[0], s0);
     if (s0 + 1 < s1) issue(lds[1], s0 + 1);
-    int cur = 0;
-    for (int s = s0; s < s1; ++s) {
-        const int refill = cur == 0 ? 2 : cur - 1;  // slot of stage s - 1 == slot of stage s + 2
-        stage(lds[cur], lds[refill], s);
-        cur = cur == 2 ? 0 : cur + 1;
+    // The slot of stage s - 1 is the slot of stage s + 2. The first stage has nothing deferred;
+    // the steady state issues and has a deferred group (no branches); the last two issue nothing.
+    int cur = 0, s = s0;
+    auto refill = [&]() { return cur == 0 ? 2 : cur - 1; };
+    auto next = [&]() { cur = cur == 2 ? 0 : cur + 1; ++s; };
+    if (s < s1) {
+        stage(lds[cur], lds[refill()], s, s + 2 < s1, false);
+        next();
     }
+    for (; s + 2 < s1; next()) stage(lds[cur], lds[refill()], s, true, true);
+    for (; s < s1; next()) stage(lds[cur], lds[refill()], s, false, true);
     if (s0 < s1) tail();
 
     // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
