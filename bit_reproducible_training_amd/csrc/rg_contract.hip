@@ -81,6 +81,9 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 #define RG_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 // s_waitcnt on LDS (and scalar memory) operations only: wait until none is outstanding.
 #define RG_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8))
+// Lambdas of the kernels hold references to register arrays: they must be inlined, or the
+// arrays would move to scratch memory.
+#define RG_INLINE __attribute__((always_inline))
 #define RG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // Wavefronts per SIMD that the block tile's LDS ring allows (blocks per CU x wavefronts per
@@ -166,7 +169,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[l][ti][tj][e] = 0;
 
-    auto issue = [&](v4i (*slot)[64], int step) {
+    auto issue = [&](v4i (*slot)[64], int step) RG_INLINE {
         const uint32_t soff = (uint32_t)(step - s0) * step_bytes;
 #pragma unroll
         for (int i = 0; i < PW; ++i)
@@ -185,15 +188,15 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // scheduling-group barriers pin the order: DS read groups (mask 0x100), VMEM groups
     // (0x020) and MFMA groups (0x008).
     v4i a[2][S][WTI], b[2][S][WTJ];
-    auto load_a = [&](v4i (*slot)[64], int kk, int p) {
+    auto load_a = [&](v4i (*slot)[64], int kk, int p) RG_INLINE {
 #pragma unroll
         for (int ti = 0; ti < WTI; ++ti) a[kk][p][ti] = slot[((wm * WTI + ti) * 2 + kk) * S + p][lane];
     };
-    auto load_b = [&](v4i (*slot)[64], int kk, int q) {
+    auto load_b = [&](v4i (*slot)[64], int kk, int q) RG_INLINE {
 #pragma unroll
         for (int tj = 0; tj < WTJ; ++tj) b[kk][q][tj] = slot[PA + ((wn * WTJ + tj) * 2 + kk) * S + q][lane];
     };
-    auto mma = [&](int kk, int p, int q) {
+    auto mma = [&](int kk, int p, int q) RG_INLINE {
 #pragma unroll
         for (int ti = 0; ti < WTI; ++ti)
 #pragma unroll
@@ -204,17 +207,17 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     constexpr int T = WTI * WTJ;  // MFMAs per digit product
     constexpr int OPEN = WTI + WTJ + (S > 1 ? WTI : 0);
     // Reads that open a k-step: a0, b0 and (S > 1) a1.
-    auto open_step = [&](v4i (*slot)[64], int kk) {
+    auto open_step = [&](v4i (*slot)[64], int kk) RG_INLINE {
         load_a(slot, kk, 0);
         load_b(slot, kk, 0);
         if (S > 1) load_a(slot, kk, 1);
     };
     // The deferred group of the previous stage: products (p, S-1) of its second k-step.
-    auto tail = [&]() {
+    auto tail = [&]() RG_INLINE {
 #pragma unroll
         for (int p = 0; p < S; ++p) mma(1, p, S - 1);
     };
-    auto compute = [&](v4i (*slot)[64], bool with_tail, v4i (*refill)[64], int s_refill, bool do_issue) {
+    auto compute = [&](v4i (*slot)[64], bool with_tail, v4i (*refill)[64], int s_refill, bool do_issue) RG_INLINE {
         if (with_tail) {
             mma(1, 0, S - 1);
             __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
@@ -272,7 +275,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // for its reads of stage s-1 (the deferred group's operands are in registers then),
     // barrier (everyone's stage s has landed and everyone's reads of stage s-1 are done, so
     // its slot can be refilled), contract stage s, issuing stage s+2 into that slot.
-    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s, bool do_issue, bool with_tail) {
+    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s, bool do_issue, bool with_tail) RG_INLINE {
         if (s + 1 < s1) RG_WAIT_VMCNT(PW);
         else RG_WAIT_VMCNT(0);
         RG_WAIT_LGKMCNT0();
@@ -288,8 +291,8 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // The slot of stage s - 1 is the slot of stage s + 2. The first stage has nothing deferred;
     // the steady state issues and has a deferred group (no branches); the last two issue nothing.
     int cur = 0, s = s0;
-    auto refill = [&]() { return cur == 0 ? 2 : cur - 1; };
-    auto next = [&]() { cur = cur == 2 ? 0 : cur + 1; ++s; };
+    auto refill = [&]() RG_INLINE { return cur == 0 ? 2 : cur - 1; };
+    auto next = [&]() RG_INLINE { cur = cur == 2 ? 0 : cur + 1; ++s; };
     if (s < s1) {
         stage(lds[cur], lds[refill()], s, s + 2 < s1, false);
         next();
