@@ -335,6 +335,7 @@ def main():
     ms = head["ms_per_step"]
     eff = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     int8_ops = S * S * 2.0 * M * N * K
+    slice_bytes = 4 * (M * K + K * N) + S * (M * K + N * K) + 4 * (M + N)
     contract_tops = int8_ops / (head["contract_ms"] * 1e-3) / 1e12
     line = {
         "metric": "effective FP32 TFLOP/s, S=3 repro GEMM 4096^3; % int8 MFMA peak; bit-exact",
@@ -361,6 +362,13 @@ def main():
                      "traffic": TRAFFIC_BYTES,
                      "kernel": "contract_mfma<3,2,1,2,4>: int8 ops = 9 * 2MNK per launch, one "
                                "launch per step; achieved = ops / HIP-event duration"},
+        # The slicing stage against the HBM roofline: algorithmic bytes = fp32 inputs read once
+        # (4(MK + KN)) + S digit planes written (S(MK + NK)) + the int32 exponents (4(M + N)),
+        # over the stage's HIP-event duration (both slicing launches and the gap between them).
+        "slicing_roofline": {"bound": "hbm", "achieved": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9, 1),
+                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                             "bytes": slice_bytes},
         "mfma_ceiling_measured": dict(ceiling, contract_frac_of_dense=round(
             contract_tops / ceiling["dense_tops"], 4) if ceiling["dense_tops"] else None),
         "cpu_baseline": cpu,
