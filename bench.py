@@ -273,6 +273,189 @@ def suite(torch, rg, reps=10, warmup=2):
           flush=True)
 
 
+# --------------------------------------------------------------------------------------
+# Beyond the GEMM: the exact sum, the convolution, the batched GEMM and the Linear layer, each
+# against its roofline and next to the times the reference recorded for its own benchmarks.
+# --------------------------------------------------------------------------------------
+# Fastest time the reference recorded per benchmark case (median ms per call, RTX 2080 Ti,
+# TITAN V, RTX 4070): repro_sum_cuda/results/*/sum.log (bench_repro_sum.cu:60-67 shapes) and
+# repro_conv_cuda/results/*/conv.log (bench_repro_conv.cu, LeNet-5, batch 100, S=3).
+REF_SUM_MS = {"vector 16M": 0.157, "conv bias grad 256x64x56x56": 0.373,
+              "linear bias grad 8192x4096": 0.313, "row sums 8192x4096": 0.253,
+              "LayerNorm-like rows 16384x1024": 0.144, "softmax-like rows 65536x128": 0.102,
+              "LeNet conv1 bias 100x6x28x28": 0.019, "LeNet softmax rows 100x10": 0.008}
+SUM_SHAPES = [("vector 16M", 1, 1, 1 << 24), ("conv bias grad 256x64x56x56", 256, 64, 3136),
+              ("linear bias grad 8192x4096", 8192, 4096, 1), ("row sums 8192x4096", 1, 8192, 4096),
+              ("LayerNorm-like rows 16384x1024", 1, 16384, 1024),
+              ("softmax-like rows 65536x128", 1, 65536, 128),
+              ("LeNet conv1 bias 100x6x28x28", 100, 6, 784), ("LeNet softmax rows 100x10", 1, 100, 10)]
+REF_CONV_MS = {("conv1", "fwd"): 0.059, ("conv1", "dW"): 0.454, ("conv1", "dX"): 0.067,
+               ("conv2", "fwd"): 0.121, ("conv2", "dW"): 0.337, ("conv2", "dX"): 0.077}
+
+
+def _gpu_ms(torch, fn, reps=20, warmup=3):
+    """GPU time per call: `reps` calls enqueued back to back between two events."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _wall_ms(torch, fn, reps=20, warmup=3):
+    """Median wall time per call including the launch and a device synchronisation: the
+    reference benchmarks' method (bench_repro_conv.cu:45-57)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        t.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(t)
+
+
+def _cpu_widened(x_sums, convs, threads):
+    """CPU baseline leg: the reference's own exact sum and convolution (oracle/_ref, built from
+    repro_sum_cuda and repro_conv_cuda) or this repository's port, timed on the host, and the
+    GPU results checked against them bit for bit."""
+    from oracle import oracle as O
+
+    os.environ["REPRO_CPU_THREADS"] = str(threads)
+    kind = "reference" if O.ref is not None else "port"
+    res = {"kind": kind, "sums": [], "conv": []}
+    for name, A, B, C, x, gpu in x_sums:
+        t0 = time.perf_counter()
+        want = O.ref_exact_sum(x, A, B, C) if kind == "reference" else O.exact_sum(x, A, B, C)
+        res["sums"].append({"case": name, "ms": round((time.perf_counter() - t0) * 1e3, 3),
+                            "bits_equal": bool(np.array_equal(want.view(np.uint32), gpu.view(np.uint32)))})
+    for name, shape, ins, gpu in convs:
+        row = {"case": name}
+        for kind_, a, b in ins:
+            t0 = time.perf_counter()
+            if kind == "reference":
+                want = O.ref_conv(kind_, a, b, shape, 3)
+            else:
+                want = {"fwd": O.conv2d, "dW": O.conv2d_grad_weight, "dX": O.conv2d_grad_input}[kind_](a, b, shape, 3)
+            row[kind_ + "_ms"] = round((time.perf_counter() - t0) * 1e3, 3)
+            row[kind_ + "_bits_equal"] = bool(np.array_equal(np.asarray(want, np.float32).view(np.uint32).ravel(),
+                                                             gpu[kind_].view(np.uint32).ravel()))
+        res["conv"].append(row)
+    res["cores"] = threads
+    return res
+
+
+def widened(torch, rg, cpu=True, threads=16):
+    """One JSON line: exact sum (GB/s against HBM), LeNet convolutions, batched attention-head
+    GEMMs and a GPT-2 Linear layer step (effective TFLOP/s), with the reference's recorded
+    times where it has them."""
+    line = {"mode": "widened", "slices": 3, "data": "synthetic N(0,1) (torch.randn, seed 0)"}
+    torch.manual_seed(0)
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    # Exact sums: x = [A][B][C], out[b] = sum over a, c (bench_repro_sum.cu's shapes).
+    sums, x_sums = [], []
+    for name, A, B, C in SUM_SHAPES:
+        x = torch.randn(A * B * C, device="cuda")
+        out = torch.empty(B, device="cuda")
+        cfg = rg.SumConfig()
+        plan = rg.make_sum_plan(A, B, C, cfg)
+        ws = torch.empty(max(plan.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
+
+        def run():
+            code = rg.repro_sum_fp32_ws(x.data_ptr(), out.data_ptr(), A, B, C, cfg, ws.data_ptr(),
+                                        ws.numel(), stream())
+            if code != 0:
+                raise rg.ReproGemmError(code, "exact sum")
+
+        ms = _gpu_ms(torch, run)
+        first = out.cpu().numpy().copy()
+        run()
+        same = bool(np.array_equal(first.view(np.uint32), out.cpu().numpy().view(np.uint32)))
+        gbs = 4.0 * A * B * C / (ms * 1e-3) / 1e9
+        sums.append({"case": name, "A": A, "B": B, "C": C, "gpu_ms": round(ms, 4),
+                     "wall_ms": round(_wall_ms(torch, run), 4), "GB/s": round(gbs, 1),
+                     "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "same_bits_every_run": same,
+                     "reference_best_gpu_ms": REF_SUM_MS.get(name)})
+        if A * B * C <= (1 << 22):
+            x_sums.append((name, A, B, C, x.cpu().numpy(), first))
+        del x, out, ws
+    line["exact_sum"] = sums
+    # LeNet-5 convolutions, batch 100 (bench_repro_conv.cu's shapes and input scales).
+    shapes = [("conv1", rg.ConvShape(100, 1, 28, 28, 6, 5, 5, 1, 1, 2, 2)),
+              ("conv2", rg.ConvShape(100, 6, 14, 14, 16, 5, 5))]
+    convs, conv_cpu = [], []
+    for name, g in shapes:
+        x = torch.randn(g.N, g.C, g.H, g.W, device="cuda")
+        w = 0.1 * torch.randn(g.F, g.C, g.KH, g.KW, device="cuda")
+        dy = 1e-3 * torch.randn(g.N, g.F, g.OH, g.OW, device="cuda")
+        y = torch.empty_like(dy)
+        dw = torch.empty_like(w)
+        dx = torch.empty_like(x)
+        row = {"case": name, "shape": list(g.astuple())}
+        outs = {}
+        for kind, fn, ws_fn, a, b, o in (("fwd", rg.repro_conv2d_ws, rg.conv2d_workspace, x, w, y),
+                                          ("dW", rg.repro_conv2d_grad_weight_ws, rg.conv2d_grad_weight_workspace, dy, x, dw),
+                                          ("dX", rg.repro_conv2d_grad_input_ws, rg.conv2d_grad_input_workspace, dy, w, dx)):
+            ws = torch.empty(max(ws_fn(g, 3), 1), dtype=torch.uint8, device="cuda")
+
+            def run():
+                code = fn(a.data_ptr(), b.data_ptr(), o.data_ptr(), g, 3, ws.data_ptr(), ws.numel(), stream())
+                if code != 0:
+                    raise rg.ReproGemmError(code, "conv " + kind)
+
+            row[kind + "_gpu_ms"] = round(_gpu_ms(torch, run), 4)
+            row[kind + "_wall_ms"] = round(_wall_ms(torch, run), 4)
+            row[kind + "_reference_best_gpu_ms"] = REF_CONV_MS[(name, kind)]
+            outs[kind] = o.cpu().numpy().copy()
+        convs.append(row)
+        conv_cpu.append((name, g.astuple(), [("fwd", x.cpu().numpy(), w.cpu().numpy()),
+                                             ("dW", dy.cpu().numpy(), x.cpu().numpy()),
+                                             ("dX", dy.cpu().numpy(), w.cpu().numpy())], outs))
+    line["conv"] = convs
+    # Attention heads as one strided-batched GEMM vs one GEMM per head (GPT-2 small: 12 heads,
+    # 1024 tokens, head size 64): scores = Q_h K_h^T and out = P_h V_h, read in place.
+    T, H, D = 1024, 12, 64
+    q, k, v = (torch.randn(T, H * D, device="cuda") for _ in range(3))
+    p = torch.rand(H, T, T, device="cuda") / T
+    heads = lambda z: z.view(T, H, D).permute(1, 0, 2)
+    att = {}
+    for name, fn_b, fn_l, flops in (
+            ("scores QK^T", lambda: rg.bmm(heads(q), heads(k), False, True),
+             lambda: [rg.gemm(q[:, h * D:(h + 1) * D].contiguous(), k[:, h * D:(h + 1) * D].contiguous(), T, T, D, False, True) for h in range(H)],
+             2.0 * H * T * T * D),
+            ("PV", lambda: rg.bmm(p, heads(v), False, False),
+             lambda: [rg.gemm(p[h], v[:, h * D:(h + 1) * D].contiguous(), T, D, T, False, False) for h in range(H)],
+             2.0 * H * T * T * D)):
+        mb, ml = _gpu_ms(torch, fn_b, reps=10), _gpu_ms(torch, fn_l, reps=10)
+        att[name] = {"batched_ms": round(mb, 4), "per_head_loop_ms": round(ml, 4),
+                     "batched_tflops": round(flops / (mb * 1e-3) / 1e12, 2)}
+    line["attention_heads"] = dict(att, heads=H, tokens=T, head_dim=D)
+    del q, k, v, p
+    # GPT-2 MLP up-projection as a reproducible Linear layer: forward + backward (dX, dW, db).
+    tok, fin, fout = 8192, 768, 3072
+    layer = rg.Linear(fin, fout).cuda()
+    xin = torch.randn(tok, fin, device="cuda", requires_grad=True)
+    gy = torch.randn(tok, fout, device="cuda")
+
+    def step():
+        y = layer(xin)
+        y.backward(gy)
+
+    ms = _gpu_ms(torch, step, reps=10)
+    line["linear_step"] = {"layer": "Linear(768, 3072), 8192 tokens, forward + backward", "ms": round(ms, 4),
+                           "effective_tflops": round(3 * 2.0 * tok * fin * fout / (ms * 1e-3) / 1e12, 2)}
+    if cpu:
+        line["cpu_baseline"] = _cpu_widened(x_sums, conv_cpu, threads)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -283,6 +466,8 @@ def main():
     ap.add_argument("--no-adversarial", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--widened", action="store_true",
+                    help="time the exact sum, convolutions, batched GEMM and Linear layer instead")
     ap.add_argument("--suite", action="store_true",
                     help="time the reference GPT-2 suite's 21 GEMMs (1024 tokens) instead")
     ap.add_argument("--calibrate", action="store_true",
@@ -301,6 +486,9 @@ def main():
 
     if args.suite:
         suite(torch, rg)
+        return
+    if args.widened:
+        widened(torch, rg, cpu=not args.no_cpu, threads=args.cpu_threads)
         return
 
     n = args.size
