@@ -133,8 +133,10 @@ sum_columns(const float* __restrict__ x, int A, int B, int rows_per_chunk, int c
     }
 }
 
-// C > 1. Wave w of block x handles output b = 4 x + w and chunk blockIdx.y: summands
-// [i0, i1) of the A*C values of b, in order a-major, walked as contiguous runs of x.
+// C > 1. Wave w of block x handles item 4 x + w of the B * chunks (output, chunk) items,
+// output b = item / chunks, chunk item % chunks: summands [i0, i1) of the A*C values of b, in
+// order a-major, walked as contiguous runs of x. Every wave of a block has work when
+// B * chunks fills the grid, however small B is.
 __global__ void __launch_bounds__(SUM_THREADS)
 sum_segments(const float* __restrict__ x, int A, int B, int C, int chunks, uint32_t divisor,
              float* __restrict__ out, int64_t* __restrict__ part, int* __restrict__ part_nf) {
@@ -142,8 +144,9 @@ sum_segments(const float* __restrict__ x, int A, int B, int C, int chunks, uint3
     __shared__ int64_t merged[4][LIMBS];
     __shared__ int nf_sh[SUM_THREADS];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int b = blockIdx.x * 4 + w;
-    const int chunk = blockIdx.y;
+    const long long item = (long long)blockIdx.x * 4 + w;
+    const int b = item < (long long)B * chunks ? (int)(item / chunks) : B;  // B: no work
+    const int chunk = b < B ? (int)(item - (long long)b * chunks) : 0;
     LdsAcc acc_t{acc + t};
     acc_t.clear();
     int nf = 0;
@@ -195,10 +198,15 @@ sum_segments(const float* __restrict__ x, int A, int B, int C, int chunks, uint3
         emit(merged[w], 1, nf_sh[64 * w], b, B, chunk, chunks, divisor, out, part, part_nf);
 }
 
-// Merges the chunks of each output (thread per output) and rounds once.
+// Merges the chunks of each output and rounds once. Few chunks: a thread per output adds
+// them; many: a block per output, thread t adding chunks t, t + 256, ... and the block
+// reducing its threads' sums. Either way the normalised limbs (each < 2^32) of at most 65535
+// chunks sum below 2^48 in int64.
+constexpr int MERGE_BLOCK_FROM = 32;
+
 __global__ void __launch_bounds__(SUM_THREADS)
-sum_merge(const int64_t* __restrict__ part, const int* __restrict__ part_nf, int B, int chunks,
-          uint32_t divisor, float* __restrict__ out) {
+sum_merge_threads(const int64_t* __restrict__ part, const int* __restrict__ part_nf, int B,
+                  int chunks, uint32_t divisor, float* __restrict__ out) {
     const int b = blockIdx.x * SUM_THREADS + threadIdx.x;
     if (b >= B) return;
     int64_t tot[LIMBS];
@@ -211,6 +219,41 @@ sum_merge(const int64_t* __restrict__ part, const int* __restrict__ part_nf, int
         nf |= part_nf[(size_t)k * B + b];
     }
     out[b] = repro_sum::finalize(tot, 1, divisor, nf);
+}
+
+__global__ void __launch_bounds__(SUM_THREADS)
+sum_merge(const int64_t* __restrict__ part, const int* __restrict__ part_nf, int B, int chunks,
+          uint32_t divisor, float* __restrict__ out) {
+    __shared__ int64_t red[LIMBS][SUM_THREADS];
+    __shared__ int nf_sh[SUM_THREADS];
+    const int b = blockIdx.x, t = threadIdx.x;
+    int64_t tot[LIMBS];
+#pragma unroll
+    for (int l = 0; l < LIMBS; ++l) tot[l] = 0;
+    int nf = 0;
+    for (int k = t; k < chunks; k += SUM_THREADS) {
+#pragma unroll
+        for (int l = 0; l < LIMBS; ++l) tot[l] += part[((size_t)k * LIMBS + l) * B + b];
+        nf |= part_nf[(size_t)k * B + b];
+    }
+#pragma unroll
+    for (int l = 0; l < LIMBS; ++l) red[l][t] = tot[l];
+    nf_sh[t] = nf;
+    __syncthreads();
+    for (int s = SUM_THREADS / 2; s > 0; s >>= 1) {
+        if (t < s) {
+#pragma unroll
+            for (int l = 0; l < LIMBS; ++l) red[l][t] += red[l][t + s];
+            nf_sh[t] |= nf_sh[t + s];
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        int64_t lim[LIMBS];
+#pragma unroll
+        for (int l = 0; l < LIMBS; ++l) lim[l] = red[l][0];
+        out[b] = repro_sum::finalize(lim, 1, divisor, nf_sh[0]);
+    }
 }
 
 // Non-finite scan (repro_torch/src/kernels.cu:8-20): one vote per wave, one atomic min per
@@ -263,9 +306,9 @@ int sum_layout(int A, int B, int C, const rg_sum_config* cfg, int num_cus, SumLa
             chunks = (target_blocks + bx - 1) / bx;
             chunks = std::min(chunks, std::max(1, A / 64));     // >= 64 rows per chunk
         } else {
-            const int blocks_x = (B + 3) / 4;
-            chunks = (target_blocks + blocks_x - 1) / blocks_x;
-            chunks = (int)std::min<long long>(chunks, std::max(1LL, count / 4096));
+            const long long target_waves = 4LL * target_blocks;      // (output, chunk) items
+            chunks = (int)std::min<long long>((target_waves + B - 1) / B, 65535);
+            chunks = (int)std::min<long long>(chunks, std::max(1LL, count / 2048));
         }
     }
     chunks = std::max(1, std::min(chunks, max_chunks));
@@ -340,14 +383,19 @@ int rg_sum_fp32_ws(const float* x, float* out, int A, int B, int C, const rg_sum
         hipLaunchKernelGGL(rg::sum_columns, grid, dim3(rg::SUM_THREADS), 0, stream, x, A, B,
                            L.rows_per_chunk, L.chunks, divisor, out, part, part_nf);
     } else {
-        dim3 grid((B + 3) / 4, L.chunks);
-        hipLaunchKernelGGL(rg::sum_segments, grid, dim3(rg::SUM_THREADS), 0, stream, x, A, B, C,
-                           L.chunks, divisor, out, part, part_nf);
+        const long long items = (long long)B * L.chunks;
+        if ((items + 3) / 4 > INT_MAX) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(rg::sum_segments, dim3((unsigned)((items + 3) / 4)), dim3(rg::SUM_THREADS),
+                           0, stream, x, A, B, C, L.chunks, divisor, out, part, part_nf);
     }
     if (L.chunks > 1) {
-        hipLaunchKernelGGL(rg::sum_merge, dim3((B + rg::SUM_THREADS - 1) / rg::SUM_THREADS),
-                           dim3(rg::SUM_THREADS), 0, stream, part, part_nf, B, L.chunks, divisor,
-                           out);
+        if (L.chunks < rg::MERGE_BLOCK_FROM)
+            hipLaunchKernelGGL(rg::sum_merge_threads, dim3((B + rg::SUM_THREADS - 1) / rg::SUM_THREADS),
+                               dim3(rg::SUM_THREADS), 0, stream, part, part_nf, B, L.chunks,
+                               divisor, out);
+        else
+            hipLaunchKernelGGL(rg::sum_merge, dim3((unsigned)B), dim3(rg::SUM_THREADS), 0, stream,
+                               part, part_nf, B, L.chunks, divisor, out);
     }
     return hipGetLastError();
 }
