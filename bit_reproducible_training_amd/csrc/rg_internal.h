@@ -87,10 +87,10 @@ struct SliceDesc {
 void slice_grid(SliceDesc& d);
 
 // Single-pass slicing (row maxima, exponents and digit panels in one launch, each input read
-// once) of an operand that allows 16-byte loads, for padded K up to ONEPASS_MAX_K (row access)
-// or ONEPASS_MAX_K_COLUMNS (column access, whose 32-byte row segments fetch slower than the
-// two passes' wide ones at large K). launch_onepass slices the operands whose use_* is set
-// (both share K).
+// once) of an operand, for padded K up to ONEPASS_MAX_K (row access) or ONEPASS_MAX_K_COLUMNS
+// (column access, whose 32-byte row segments fetch slower than the two passes' wide ones at
+// large K); 16-byte loads where the operand allows them, scalar loads otherwise.
+// launch_onepass slices the operands whose use_* is set (both share K).
 constexpr int ONEPASS_MAX_K = 4096;
 constexpr int ONEPASS_MAX_K_COLUMNS = 3072;
 bool onepass_eligible(const SliceDesc& d);

@@ -34,9 +34,26 @@ __device__ __forceinline__ float max4(float4 v) {
 
 // Row access, element (r, k) of item b at src[b*bstride + r*ld + k]: wavefront w of the
 // operand handles row w / nch of all items' rows (item-major), chunk w % nch.
+// (row, chunk) pairs per wavefront in the row-access maxima: a lane per pair for short
+// chunks (a wavefront per pair would leave most lanes idle), else the whole wavefront.
+__host__ __device__ inline int rows_per_wave(const SliceDesc& d) { return d.kch <= 32 ? 64 : 1; }
+
 template <int WAVES>
 __device__ void absmax_rows(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63;
+    if (rows_per_wave(d) > 1) {
+        const long long pair = (blk * WAVES + (threadIdx.x >> 6)) * 64 + lane;
+        if (pair >= (long long)d.batch * d.R * d.nch) return;
+        const long long i = pair / d.nch;
+        const int c = (int)(pair - i * d.nch);
+        const int b = (int)(i / d.R), r = (int)(i - (long long)b * d.R);
+        const int k0 = c * d.kch, k1 = min(d.K, k0 + d.kch);
+        const float* row = d.src + (size_t)b * d.bstride + (size_t)r * d.ld;
+        float m = 0.0f;
+        for (int k = k0; k < k1; ++k) m = fmaxf(m, fabsf(row[k]));
+        d.pmax[(size_t)c * d.batch * d.Rp + (size_t)b * d.Rp + r] = m;
+        return;
+    }
     const long long w = blk * WAVES + (threadIdx.x >> 6);
     if (w >= (long long)d.batch * d.R * d.nch) return;
     const long long i = w / d.nch;
@@ -394,7 +411,11 @@ __global__ void __launch_bounds__(256) split_kernel(SliceDesc a, SliceDesc b) {
 // the wavefront's LDS tile. Blocks blk, blk+8, blk+16, blk+24, which the dispatcher places on
 // the same XCD, take four neighbouring strips, so a column-access operand's 128-byte lines
 // (32 columns) are fetched into one L2 once.
-template <int S, int NF4>
+//
+// Wave-strip form (WS, padded K <= 256, NF4 = its k-panels): each wavefront owns its own strip
+// (strip 8 blk + w) over all of K, so short rows keep all 8 wavefronts busy; the maxima are
+// then reduced within the wavefront only and no block barrier is needed.
+template <int S, int NF4, bool WS = false>
 __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][8];
     __shared__ int sse[8];
@@ -402,16 +423,17 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int per_item = d.Rp / 8;
     const long long nstrips = (long long)d.batch * per_item;
-    const long long st = (blk >> 5) * 32 + (blk & 7) * 4 + ((blk >> 3) & 3);
-    if (st >= nstrips) return;
+    const long long st = WS ? blk * 8 + w : (blk >> 5) * 32 + (blk & 7) * 4 + ((blk >> 3) & 3);
+    if (st >= nstrips) return;  // the whole block (a whole wavefront for WS)
     const int item = (int)(st / per_item);
     const int r0 = (int)(st - (long long)item * per_item) * 8;  // first row within the item
     const int rp = (item * d.Rp + r0) / PANEL_ROWS;              // stacked 32-row panel
     const int r_in = r0 & 24;                                    // strip offset in the panel
     const float* base = d.src + (size_t)item * d.bstride;
-    const int kp0 = w * NF4;                                     // this wavefront's first k-panel
+    const int kp0 = WS ? 0 : w * NF4;                            // this wavefront's first k-panel
     const int npk = d.Kp / PANEL_K;
     float4 v[NF4];
+    float wmax = 0.0f;
     if (!d.strided) {
         const int row = r0 + (lane >> 3);
         float m = 0.0f;
@@ -419,13 +441,24 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
         for (int i = 0; i < NF4; ++i) {
             const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
             v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (row < d.R && k < d.K) v[i] = *reinterpret_cast<const float4*>(base + (size_t)row * d.ld + k);
+            if (row < d.R && k < d.K) {
+                const float* q = base + (size_t)row * d.ld + k;
+                if (d.vec) {
+                    v[i] = *reinterpret_cast<const float4*>(q);
+                } else {  // unaligned rows or K % 4 != 0: four scalar loads inside K
+                    v[i].x = q[0];
+                    if (k + 1 < d.K) v[i].y = q[1];
+                    if (k + 2 < d.K) v[i].z = q[2];
+                    if (k + 3 < d.K) v[i].w = q[3];
+                }
+            }
         }
 #pragma unroll
         for (int i = 0; i < NF4; ++i) m = fmaxf(m, max4(v[i]));
 #pragma unroll
         for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        if ((lane & 7) == 0) smax[w][lane >> 3] = m;
+        if (WS) wmax = m;  // lanes 8j..8j+7 all hold row j's maximum
+        else if ((lane & 7) == 0) smax[w][lane >> 3] = m;
     } else {
         const int c = r0 + 4 * (lane & 1);
         float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -433,7 +466,17 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
         for (int i = 0; i < NF4; ++i) {
             const int k = (kp0 + i) * PANEL_K + (lane >> 1);
             v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (k < d.K && c < d.R) v[i] = *reinterpret_cast<const float4*>(base + (size_t)k * d.ld + c);
+            if (k < d.K && c < d.R) {
+                const float* q = base + (size_t)k * d.ld + c;
+                if (d.vec) {
+                    v[i] = *reinterpret_cast<const float4*>(q);
+                } else {  // unaligned or R % 4 != 0: four scalar loads inside R
+                    v[i].x = q[0];
+                    if (c + 1 < d.R) v[i].y = q[1];
+                    if (c + 2 < d.R) v[i].z = q[2];
+                    if (c + 3 < d.R) v[i].w = q[3];
+                }
+            }
         }
 #pragma unroll
         for (int i = 0; i < NF4; ++i) {
@@ -449,27 +492,38 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
             m.z = fmaxf(m.z, __shfl_xor(m.z, off, 64));
             m.w = fmaxf(m.w, __shfl_xor(m.w, off, 64));
         }
-        if (lane < 2) {
+        if (WS) {  // column lane/8 of the strip: component (lane/8) % 4 of lane (lane/8) / 4
+            const int c = lane >> 3;
+            const float mx = __shfl(m.x, c >> 2, 64), my = __shfl(m.y, c >> 2, 64);
+            const float mz = __shfl(m.z, c >> 2, 64), mw = __shfl(m.w, c >> 2, 64);
+            wmax = (c & 3) == 0 ? mx : (c & 3) == 1 ? my : (c & 3) == 2 ? mz : mw;
+        } else if (lane < 2) {
             smax[w][4 * lane + 0] = m.x;
             smax[w][4 * lane + 1] = m.y;
             smax[w][4 * lane + 2] = m.z;
             smax[w][4 * lane + 3] = m.w;
         }
     }
-    __syncthreads();
-    if (threadIdx.x < 8) {
-        float m = smax[0][threadIdx.x];
+    int lane_se = 0;  // WS: exponent of this lane's row (row or column lane / 8 of the strip)
+    if (WS) {
+        lane_se = scale_exponent(wmax);  // rows >= R have a zero maximum, so exponent 0
+        if ((lane & 7) == 0) d.expo[(size_t)item * d.Rp + r0 + (lane >> 3)] = lane_se;
+    } else {
+        __syncthreads();
+        if (threadIdx.x < 8) {
+            float m = smax[0][threadIdx.x];
 #pragma unroll
-        for (int i = 1; i < 8; ++i) m = fmaxf(m, smax[i][threadIdx.x]);
-        const int se = scale_exponent(m);  // rows >= R have m == 0, so se == 0
-        sse[threadIdx.x] = se;
-        d.expo[(size_t)item * d.Rp + r0 + threadIdx.x] = se;
+            for (int i = 1; i < 8; ++i) m = fmaxf(m, smax[i][threadIdx.x]);
+            const int se = scale_exponent(m);  // rows >= R have m == 0, so se == 0
+            sse[threadIdx.x] = se;
+            d.expo[(size_t)item * d.Rp + r0 + threadIdx.x] = se;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     // Output word of lane (row or column ro of the strip, 16-k half h, word wd) in panel kp.
     uint32_t* out = static_cast<uint32_t*>(d.out);
     const int ro = lane >> 3, h = (lane >> 2) & 1, wd = lane & 3;
-    const RowScale rs = row_scale<S>(sse[ro]);
+    const RowScale rs = row_scale<S>(WS ? lane_se : sse[ro]);
     uint32_t* o0 = out + (size_t)rp * npk * S * (PANEL_BYTES / 4) + 4 * (r_in + ro + 32 * h) + wd;
     float (*tile)[33] = tr[w];
 #pragma unroll
@@ -511,11 +565,11 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     }
 }
 
-template <int S, int NF4>
+template <int S, int NF4, bool WS>
 __global__ void __launch_bounds__(512) slice_onepass_kernel(SliceDesc a, SliceDesc b, long long a_blocks) {
     const long long blk = blockIdx.x;
-    if (blk < a_blocks) slice_onepass<S, NF4>(a, blk);
-    else slice_onepass<S, NF4>(b, blk - a_blocks);
+    if (blk < a_blocks) slice_onepass<S, NF4, WS>(a, blk);
+    else slice_onepass<S, NF4, WS>(b, blk - a_blocks);
 }
 
 // The one pass of operand `one` fused with the partial maxima (first of the two passes) of
@@ -532,7 +586,8 @@ __global__ void __launch_bounds__(512) onepass_absmax_kernel(SliceDesc one, Slic
 // Blocks of the partial-maxima pass of d with 8 wavefronts per block.
 static long long absmax8_blocks(const SliceDesc& d) {
     if (d.strided) return d.max_blocks;  // one block per (item, column group, chunk)
-    return ((long long)d.batch * d.R * d.nch + 7) / 8;
+    const long long per_block = 8LL * rows_per_wave(d);
+    return ((long long)d.batch * d.R * d.nch + per_block - 1) / per_block;
 }
 
 // Blocks of the one-pass slicing for one operand: its 8-row strips, rounded up to a multiple
@@ -543,18 +598,40 @@ static long long onepass_blocks(const SliceDesc& d) {
 }
 
 bool onepass_eligible(const SliceDesc& d) {
-    return d.vec && d.Kp <= (d.strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K);
+    return d.Kp <= (d.strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K);
 }
 
 void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
                     hipStream_t stream) {
+    const int kp = use_a ? a.Kp : b.Kp;
+    if (kp <= 256) {  // wave strips: 8 strips per block
+        const long long na = use_a ? ((long long)a.batch * (a.Rp / 8) + 7) / 8 : 0;
+        const long long nb = use_b ? ((long long)b.batch * (b.Rp / 8) + 7) / 8 : 0;
+        if (na + nb == 0) return;
+        const unsigned blocks = (unsigned)(na + nb);
+        const int nf4 = kp <= 64 ? 2 : (kp <= 128 ? 4 : 8);
+#define RG_ONEPASS_WS(SS, NF) slice_onepass_kernel<SS, NF, true><<<blocks, 512, 0, stream>>>(a, b, na)
+        switch (S * 100 + nf4) {
+            case 102: RG_ONEPASS_WS(1, 2); break;
+            case 104: RG_ONEPASS_WS(1, 4); break;
+            case 108: RG_ONEPASS_WS(1, 8); break;
+            case 202: RG_ONEPASS_WS(2, 2); break;
+            case 204: RG_ONEPASS_WS(2, 4); break;
+            case 208: RG_ONEPASS_WS(2, 8); break;
+            case 302: RG_ONEPASS_WS(3, 2); break;
+            case 304: RG_ONEPASS_WS(3, 4); break;
+            case 308: RG_ONEPASS_WS(3, 8); break;
+            default: break;
+        }
+#undef RG_ONEPASS_WS
+        return;
+    }
     const long long na = use_a ? onepass_blocks(a) : 0;
     const long long nb = use_b ? onepass_blocks(b) : 0;
     if (na + nb == 0) return;
     const unsigned blocks = (unsigned)(na + nb);
-    const int kp = use_a ? a.Kp : b.Kp;
     const int nf4 = kp <= 1024 ? 4 : (kp <= 2048 ? 8 : 16);
-#define RG_ONEPASS(SS, NF) slice_onepass_kernel<SS, NF><<<blocks, 512, 0, stream>>>(a, b, na)
+#define RG_ONEPASS(SS, NF) slice_onepass_kernel<SS, NF, false><<<blocks, 512, 0, stream>>>(a, b, na)
     switch (S * 100 + nf4) {
         case 104: RG_ONEPASS(1, 4); break;
         case 108: RG_ONEPASS(1, 8); break;
@@ -596,7 +673,8 @@ void slice_grid(SliceDesc& d) {
         const int cols = d.vec ? 256 : 64;
         d.max_blocks = (long long)d.batch * ((d.R + cols - 1) / cols) * d.nch;
     } else {
-        d.max_blocks = ((long long)d.batch * d.R * d.nch + 3) / 4;
+        const long long per_block = 4LL * rows_per_wave(d);
+        d.max_blocks = ((long long)d.batch * d.R * d.nch + per_block - 1) / per_block;
     }
     const int npk = d.Kp / PANEL_K;
     d.split_blocks = (long long)d.batch * (d.Rp / PANEL_ROWS) *

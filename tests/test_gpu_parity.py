@@ -145,11 +145,13 @@ def test_slicing_kernel_digits_and_exponents(torch_gpu, S, ta, tb):
         assert not e[Xo.shape[0]:].any()
 
 
-# Shapes that route the slicing through each of its paths: one pass for rows (16-byte loads,
-# padded K <= 4096) and columns (padded K <= 3072), the fused one-pass + maxima launch when
-# only one operand qualifies (with row or column maxima for the other), and two passes.
+# Shapes that route the slicing through each of its paths: one pass for rows (padded K <=
+# 4096) and columns (padded K <= 3072), with 16-byte or scalar loads, in the wave-strip form
+# for padded K <= 256; the fused one-pass + maxima launch when only one operand qualifies (with
+# row or column maxima for the other); and two passes.
 SLICE_ROUTES = [(96, 68, 1000), (100, 64, 2052), (64, 100, 3076), (68, 96, 4100),
-                (96, 64, 1001), (97, 70, 1536), (128, 64, 4096)]
+                (96, 64, 1001), (97, 70, 1536), (128, 64, 4096), (96, 68, 200), (97, 70, 61),
+                (64, 100, 128), (33, 9, 25)]
 
 
 @pytest.mark.parametrize("M,N,K", SLICE_ROUTES)
@@ -162,7 +164,7 @@ def test_slicing_routes_digits_exponents_and_result(torch_gpu, M, N, K, ta, tb):
     A = (rng.standard_normal(M * K) * 2.0 ** rng.integers(-20, 20, M * K)).astype(np.float32)
     B = rng.standard_normal(N * K).astype(np.float32)
     A[:K] = 0.0
-    for S in ((1, 2, 3) if K in (1000, 2052) else (3,)):
+    for S in ((1, 2, 3) if K in (1000, 2052, 200) else (3,)):
         X, Y, eA, eB = O.quantize(A, B, M, N, K, ta, tb, S)
         cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb)
         note("slice route M=%d N=%d K=%d ta=%d tb=%d S=%d" % (M, N, K, ta, tb, S))
