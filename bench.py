@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 # HBM bytes per launch of the contraction at 4096^3 S=3 (fetch + write), from rocprofv3
 # FETCH_SIZE / WRITE_SIZE scaled by the same counters on a 256 MiB device copy; see
 # profiles/contract_mfma_4096cube_traffic.md. Updated when the kernel changes.
-TRAFFIC_BYTES = 671529779
+TRAFFIC_BYTES = 671529280
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
