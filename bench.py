@@ -178,17 +178,22 @@ def time_workload(torch, rg, A, B, n, steps, warmup, calibrate=False):
 
     for _ in range(warmup):
         step()
-    # Timed region: exactly `steps` GEMMs; stage events on the launch stream give the
-    # contraction kernel's own duration (event 1 -> event 2 brackets only that launch).
+    # Timed region: exactly `steps` GEMMs as a caller runs them (no instrumentation).
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # Stage breakdown from a second pass of `steps` GEMMs with the stage events on the launch
+    # stream: event 1 -> event 2 brackets only the contraction kernel's launch.
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     for e in (x for row in evs for x in row):
         e.record()  # torch creates the HIP event on first record
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         step([e.cuda_event for e in evs[i]])
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     if calibrate:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -460,7 +465,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-adversarial", action="store_true")
