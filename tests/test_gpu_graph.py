@@ -1,0 +1,104 @@
+"""The asynchronous entry points inside HIP graphs (torch.cuda.graph capture).
+
+They allocate nothing, synchronise nothing and clear no memory with memset nodes, so a caller
+can capture them (serving loops, training steps replayed as graphs). Every replay must give the
+bits of the eager call on the same inputs; replays are separated by eager work and device
+synchronisations, and one replay runs on new input values written in place.
+"""
+import numpy as np
+import pytest
+
+import bit_reproducible_training_amd as rg
+from gpu_util import note
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+def _capture(torch, fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                          # warm-up outside the capture (device facts cached)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,split", [(384, 320, 1000, 0, 0, 1), (200, 130, 5000, 1, 0, 3),
+                                               (256, 64, 4096, 0, 1, 1), (1024, 1024, 64, 0, 1, 1)])
+def test_gemm_replays_equal_eager(torch_gpu, M, N, K, ta, tb, split):
+    torch = torch_gpu
+    torch.manual_seed(M + N + K)
+    A = torch.randn(M * K, device="cuda")
+    B = torch.randn(K * N, device="cuda")
+    C = torch.empty(M, N, device="cuda")
+    cfg = rg.Config(trans_a=ta, trans_b=tb, split_k=split)
+    plan = rg.make_plan(M, N, K, cfg)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+
+    def call():
+        code = rg.repro_gemm_fp32_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, cfg,
+                                     ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+        assert code == 0
+
+    note("graph gemm", M, N, K, ta, tb, split)
+    g = _capture(torch, call)
+    want = O.cpu_gemm(A.cpu().numpy(), B.cpu().numpy(), M, N, K, ta, tb, 3).view(np.uint32)
+    for rep in range(3):
+        C.fill_(float("nan"))
+        ws.zero_()                     # eager work on the same buffers between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(C), want), rep
+    A.copy_(torch.randn(M * K, device="cuda") * 3.0)
+    g.replay()
+    torch.cuda.synchronize()
+    want2 = O.cpu_gemm(A.cpu().numpy(), B.cpu().numpy(), M, N, K, ta, tb, 3).view(np.uint32)
+    assert np.array_equal(_bits(C), want2)
+
+
+def test_batched_and_sum_replays_equal_eager(torch_gpu):
+    torch = torch_gpu
+    torch.manual_seed(7)
+    T, H, D = 256, 4, 64
+    q = torch.randn(T, H * D, device="cuda")
+    k = torch.randn(T, H * D, device="cuda")
+    heads = lambda z: z.view(T, H, D).permute(1, 0, 2)
+    scores = torch.empty(H, T, T, device="cuda")
+    x = torch.randn(3000, 96, device="cuda")
+    bias_grad = torch.empty(96, device="cuda")
+    scfg = rg.SumConfig()
+    splan = rg.make_sum_plan(3000, 96, 1, scfg)
+    sws = torch.empty(max(splan.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
+
+    def call():
+        rg.bmm(heads(q), heads(k), False, True, out=scores)
+        code = rg.repro_sum_fp32_ws(x.data_ptr(), bias_grad.data_ptr(), 3000, 96, 1, scfg,
+                                    sws.data_ptr(), sws.numel(), torch.cuda.current_stream().cuda_stream)
+        assert code == 0
+
+    note("graph bmm + sum")
+    g = _capture(torch, call)
+    qn, kn, xn = q.cpu().numpy(), k.cpu().numpy(), x.cpu().numpy()
+    want_s = np.stack([O.cpu_gemm(np.ascontiguousarray(qn[:, h * D:(h + 1) * D]),
+                                  np.ascontiguousarray(kn[:, h * D:(h + 1) * D]), T, T, D, 0, 1, 3)
+                       for h in range(H)]).view(np.uint32)
+    want_b = O.exact_sum(xn, 3000, 96, 1).view(np.uint32)
+    for rep in range(3):
+        scores.fill_(float("nan"))
+        bias_grad.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(scores), want_s), rep
+        assert np.array_equal(_bits(bias_grad), want_b), rep
