@@ -44,14 +44,18 @@ int max_steps_per_part(int S) {
 
 // Row-max pass chunking, from shapes only (so the workspace size never depends on pointer
 // alignment): enough blocks to keep HBM busy, at most 16 (row access) or 32 (column access)
-// partial maxima per row, chunk lengths a multiple of 4 for float4 loads.
-void choose_chunks(int R, int K, bool strided, int* nch, int* kch) {
+// partial maxima per row, chunk lengths a multiple of 4 for float4 loads. A column-access
+// operand of at most 32 columns per item (read as whole rows, few blocks per chunk) takes up
+// to 256 chunks of at least 256 k. R is the item's row count, rows all items' rows.
+void choose_chunks(int R, int rows, int K, bool strided, int* nch, int* kch) {
     int n;
-    if (strided) {
-        int groups = ceil_div(R, R % 4 == 0 ? 256 : 64);
+    if (strided && R <= 32) {
+        n = std::min(256, ceil_div(K, 256));
+    } else if (strided) {
+        int groups = ceil_div(rows, rows % 4 == 0 ? 256 : 64);
         n = std::min(ceil_div(1024, groups), std::min(32, ceil_div(K, 16)));
     } else {
-        n = std::min(ceil_div(2048, R), std::min(16, ceil_div(K, 256)));
+        n = std::min(ceil_div(2048, rows), std::min(16, ceil_div(K, 256)));
     }
     n = std::max(1, n);
     *kch = round_up(ceil_div(K, n), 4);
@@ -179,8 +183,8 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
 
     const int rows_a = (int)std::min<long long>((long long)M * batch, 1 << 30);
     const int rows_b = (int)std::min<long long>((long long)N * batch, 1 << 30);
-    choose_chunks(rows_a, K, L.a_strided, &L.nch_a, &L.kch_a);
-    choose_chunks(rows_b, K, L.b_strided, &L.nch_b, &L.kch_b);
+    choose_chunks(M, rows_a, K, L.a_strided, &L.nch_a, &L.kch_a);
+    choose_chunks(N, rows_b, K, L.b_strided, &L.nch_b, &L.kch_b);
 
     const size_t q_elem = L.algo == RG_ALGO_REFERENCE ? sizeof(int32_t) : (size_t)S;
     const size_t Mt = (size_t)L.Mp * batch, Nt = (size_t)L.Np * batch;  // stacked rows

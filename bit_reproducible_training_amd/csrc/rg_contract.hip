@@ -401,23 +401,46 @@ contract_reference(const int32_t* __restrict__ X, const int32_t* __restrict__ Y,
     partial[(((size_t)item * split + part) * M + r) * N + c] = t;
 }
 
-// Sums the split partials in int64 (order irrelevant: exact) and rounds once; one thread per
-// output of every item.
+// Sums the split partials in int64 (order irrelevant: exact) and rounds once. TPO threads share
+// an output: each sums every TPO-th part, and the block adds their sums in LDS, so that a few
+// outputs with many parts (a long K over a small M x N) still spread over the GPU instead of
+// leaving one thread a long chain of dependent loads. Consecutive threads take consecutive
+// outputs, so every load instruction reads consecutive int64 partials.
+template <int TPO>
 __global__ void __launch_bounds__(256)
 reduce_round(const int64_t* __restrict__ partial, const int* __restrict__ eA,
              const int* __restrict__ eB, float* __restrict__ C, int M, int N, int split, int e0,
              int batch, int Mp, int Np, long long ldc, long long c_item) {
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    constexpr int OPB = 256 / TPO;  // outputs per block
+    const int t = threadIdx.x;
+    const int ol = t % OPB, sub = t / OPB;
+    const size_t idx = (size_t)blockIdx.x * OPB + ol;
     const size_t MN = (size_t)M * N;
-    if (idx >= MN * batch) return;
-    const int item = (int)(idx / MN);
-    const size_t rc = idx - (size_t)item * MN;
-    const int r = (int)(rc / N), c = (int)(rc % N);
-    const int64_t* p0 = partial + (size_t)item * split * MN + rc;
-    int64_t t = 0;
-    for (int p = 0; p < split; ++p) t += p0[(size_t)p * MN];
-    C[(size_t)item * c_item + (size_t)r * ldc + c] =
-        round_output(t, eA[(size_t)item * Mp + r] + eB[(size_t)item * Np + c] + e0);
+    const bool live = idx < MN * batch;
+    int item = 0;
+    size_t rc = 0;
+    int64_t acc = 0;
+    if (live) {
+        item = (int)(idx / MN);
+        rc = idx - (size_t)item * MN;
+        const int64_t* p0 = partial + (size_t)item * split * MN + rc;
+        for (int p = sub; p < split; p += TPO) acc += p0[(size_t)p * MN];
+    }
+    if (TPO > 1) {
+        __shared__ int64_t red[256];
+        red[t] = acc;
+#pragma unroll
+        for (int s = TPO / 2; s >= 1; s >>= 1) {
+            __syncthreads();
+            if (sub < s) red[t] += red[t + s * OPB];
+        }
+        acc = red[t];  // complete for sub == 0, which wrote it last
+    }
+    if (live && sub == 0) {
+        const int r = (int)(rc / N), c = (int)(rc % N);
+        C[(size_t)item * c_item + (size_t)r * ldc + c] =
+            round_output(acc, eA[(size_t)item * Mp + r] + eB[(size_t)item * Np + c] + e0);
+    }
 }
 
 // Test hooks: the epilogue roundings on arrays. levels: n x (2S-1) int32, most significant
@@ -492,10 +515,23 @@ void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t
 void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,
                          float* C, OutAddr out, hipStream_t stream) {
     const size_t total = (size_t)L.M * L.N * L.batch;
-    unsigned blocks = (unsigned)((total + 255) / 256);
-    reduce_round<<<blocks, 256, 0, stream>>>(partial, ea, eb, C, L.M, L.N, L.split,
-                                             -14 * (L.S - 1), L.batch, L.Mp, L.Np, out.ldc,
-                                             out.c_item);
+    // Threads per output: enough for about 2^18 threads in all, at most 256, no more than the
+    // parts.
+    int tpo = 1;
+    while (tpo < 256 && tpo < L.split && total * tpo < ((size_t)1 << 18)) tpo *= 4;
+    const unsigned blocks = (unsigned)((total * tpo + 255) / 256);
+#define RG_REDUCE(T)                                                                            \
+    reduce_round<T><<<blocks, 256, 0, stream>>>(partial, ea, eb, C, L.M, L.N, L.split,         \
+                                                -14 * (L.S - 1), L.batch, L.Mp, L.Np, out.ldc, \
+                                                out.c_item)
+    switch (tpo) {
+        case 1: RG_REDUCE(1); break;
+        case 4: RG_REDUCE(4); break;
+        case 16: RG_REDUCE(16); break;
+        case 64: RG_REDUCE(64); break;
+        default: RG_REDUCE(256); break;
+    }
+#undef RG_REDUCE
 }
 
 }  // namespace rg

@@ -184,6 +184,38 @@ def test_slicing_routes_digits_exponents_and_result(torch_gpu, M, N, K, ta, tb):
         assert np.array_equal(bits(C), O.cpu_gemm(A, B, M, N, K, ta, tb, S).view(np.uint32))
 
 
+# Narrow column-access operands (at most 32 columns per item, whose maxima pass reads whole
+# rows) over a K too long for the one-pass slicing, with split counts up to one part per
+# pipeline stage: the split-K reduction then gives each of the few outputs several threads.
+NARROW = [(6, 25, 20000), (1, 3, 9000), (2, 32, 5000), (17, 5, 12345), (32, 32, 8192)]
+
+
+@pytest.mark.parametrize("M,N,K", NARROW)
+@pytest.mark.parametrize("ta,tb", [(1, 0), (0, 0), (1, 1)])
+def test_narrow_operands_long_k(torch_gpu, M, N, K, ta, tb):
+    torch = torch_gpu
+    rng = np.random.default_rng(M * 5 + N * 11 + K + ta * 2 + tb)
+    A = (rng.standard_normal(M * K) * 2.0 ** rng.integers(-30, 30, M * K)).astype(np.float32)
+    B = rng.standard_normal(N * K).astype(np.float32)
+    B[rng.integers(0, N * K, 5)] = 1e20
+    X, Y, eA, eB = O.quantize(A, B, M, N, K, ta, tb, 3)
+    want = O.cpu_gemm(A, B, M, N, K, ta, tb, 3).view(np.uint32)
+    dA, dB = to_dev(torch, A), to_dev(torch, B)
+    nsteps = (K + 63) // 64
+    for split in (1, 7, 64, nsteps):
+        cfg = rg.Config(split_k=split, trans_a=ta, trans_b=tb)
+        note("narrow M=%d N=%d K=%d ta=%d tb=%d split=%d" % (M, N, K, ta, tb, split))
+        C, plan, ws = run(torch, dA, dB, M, N, K, cfg)
+        assert split == 1 or plan.split_k == split
+        info = rg.workspace_layout(M, N, K, cfg)
+        w = ws.cpu().numpy()
+        for R, eo, eoff in ((info.Mp, eA, info.ea), (info.Np, eB, info.eb)):
+            assert np.array_equal(w[eoff:eoff + 4 * R].view(np.int32)[:eo.shape[0]], eo)
+        _, Xg = decode_digits(w, info.qa, info.Mp, info.Kp, 3)
+        assert np.array_equal(Xg[:M, :K], X)
+        assert np.array_equal(bits(C), want), (split, plan.split_k)
+
+
 @pytest.mark.parametrize("split", [2, 3])
 def test_contraction_exact_products(torch_gpu, split):
     """Stage check of the contraction: the int64 split-K partials sum to the exact
