@@ -128,6 +128,15 @@ _SIGNATURES = {
     "rg_conv2d_ws": _CONV_RUN,
     "rg_conv2d_grad_weight_ws": _CONV_RUN,
     "rg_conv2d_grad_input_ws": _CONV_RUN,
+    "rg_conv2d_algo": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(rg_conv_shape), ctypes.c_int,
+                                      ctypes.POINTER(ctypes.c_int)]),
+    "rg_conv2d_algo_workspace": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(rg_conv_shape),
+                                                ctypes.c_int, ctypes.c_int,
+                                                ctypes.POINTER(ctypes.c_size_t)]),
+    "rg_conv2d_algo_ws": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.POINTER(rg_conv_shape),
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_size_t, ctypes.c_void_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

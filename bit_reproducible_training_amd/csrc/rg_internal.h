@@ -10,6 +10,45 @@
 
 namespace rg {
 
+// Per-row constants of the rounding X = RNE(x * 2^(7(S-1) - se)), clamped to +-lim.
+// The scale is applied as two multiplications by normal powers of two, as the definition
+// does (repro_gemm_math.cuh:44-55, 71-83): with n = 7(S-1) - se in [-122, 163], both
+// factors are normal; the product is exact unless it is subnormal, and then |v| < 2^-126
+// rounds to 0 whatever the intermediate rounding was. Needs IEEE f32 denormals, which the
+// gfx950 kernels of this library run with (denorm mode 3, no flushing).
+struct RowScale {
+    float p1, p2;
+    int lim;
+};
+
+__device__ __forceinline__ RowScale row_scale(int S, int se) {
+    const int n = 7 * (S - 1) - se;
+    const int n1 = n >> 1, n2 = n - n1;
+    RowScale rs;
+    rs.p1 = __uint_as_float((uint32_t)(n1 + 127) << 23);
+    rs.p2 = __uint_as_float((uint32_t)(n2 + 127) << 23);
+    rs.lim = 127 << (7 * (S - 1));
+    return rs;
+}
+
+template <int S>
+__device__ __forceinline__ RowScale row_scale(int se) {
+    return row_scale(S, se);
+}
+
+__device__ __forceinline__ int round_fixed(float x, const RowScale& rs) {
+    const float v = (x * rs.p1) * rs.p2;
+    const int X = (int)__builtin_rintf(v);  // v_rndne_f32: nearest-even; |v| < 2^22 here
+    return min(max(X, -rs.lim), rs.lim);
+}
+
+// Largest |x| over a 64-lane wavefront, in every lane.
+__device__ __forceinline__ float wave_max(float m) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    return m;
+}
+
 // Sliced operands are stored in 1 KiB panels of 32 rows x 32 k x one digit, in the
 // order the CDNA4 MFMA reads its operands: byte lane*16 + j of a panel holds element
 // (row = lane % 32, k = 16 * (lane / 32) + j). Panels are laid out

@@ -6,7 +6,8 @@
 //   absmax_kernel  partial max|x| of every row of op(X) over chunks of K. Row access: one
 //                  64-lane wavefront per (row, chunk), float4 loads, reduced with lane
 //                  shuffles. Column access: a block covers 256 columns (float4 per lane)
-//                  or 64 (scalar), its 4 wavefronts split the chunk's k, reduced in LDS.
+//                  or 64 (scalar), its 4 wavefronts split the chunk's k, reduced in LDS;
+//                  an operand of at most 32 columns has each wavefront read whole rows.
 //   split_kernel   a block owns one 32-row panel and 4*G consecutive 32-k panels: it
 //                  reduces the rows' partial maxima once (in LDS), computes scale_exponent,
 //                  and each wavefront rounds 16 elements per lane per panel to the
@@ -22,11 +23,6 @@ using repro_gemm::scale_exponent;
 
 constexpr int SPLIT_G = 4;  // k panels per wavefront in split_kernel
 
-__device__ __forceinline__ float wave_max(float m) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    return m;
-}
 
 __device__ __forceinline__ float max4(float4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -128,6 +124,29 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
                 m.w = fmaxf(m.w, fabsf(a.w));
             }
         }
+    } else if (d.R <= 32) {
+        // Narrow operand (one group): lane L covers column L % cpr of row L / cpr of a strip of
+        // 64 / cpr consecutive k (cpr: R rounded up to a power of two), so one load
+        // instruction reads whole rows rather than R scalars of one row.
+        int cpr = 1;
+        while (cpr < d.R) cpr <<= 1;
+        const int rpw = 64 / cpr, col = lane & (cpr - 1);
+        const int step = WAVES * rpw;
+        if (col < d.R) {
+            const float* base = item + col;
+            int k = k0 + wv * rpw + lane / cpr;
+            for (; k + 7 * step < k1; k += 8 * step) {
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = fabsf(base[(size_t)(k + i * step) * d.ld]);
+                m.x = fmaxf(m.x, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+                m.y = fmaxf(m.y, fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+            }
+            for (; k < k1; k += step) m.x = fmaxf(m.x, fabsf(base[(size_t)k * d.ld]));
+            m.x = fmaxf(m.x, m.y);
+        }
+        // Lanes of one column differ in the bits at and above cpr.
+        for (int off = cpr; off < 64; off <<= 1) m.x = fmaxf(m.x, __shfl_xor(m.x, off));
     } else {
         const int r = g * 64 + lane;
         if (r < d.R) {
@@ -173,34 +192,6 @@ __global__ void __launch_bounds__(256) absmax_kernel(SliceDesc a, SliceDesc b) {
     } else {
         if (b.strided) absmax_cols<4>(b, blk - a.max_blocks); else absmax_rows<4>(b, blk - a.max_blocks);
     }
-}
-
-// Per-row constants of the rounding X = RNE(x * 2^(7(S-1) - se)), clamped to +-lim.
-// The scale is applied as two multiplications by normal powers of two, as the definition
-// does (repro_gemm_math.cuh:44-55, 71-83): with n = 7(S-1) - se in [-122, 163], both
-// factors are normal; the product is exact unless it is subnormal, and then |v| < 2^-126
-// rounds to 0 whatever the intermediate rounding was. Needs IEEE f32 denormals, which the
-// gfx950 kernels of this library run with (denorm mode 3, no flushing).
-struct RowScale {
-    float p1, p2;
-    int lim;
-};
-
-template <int S>
-__device__ __forceinline__ RowScale row_scale(int se) {
-    const int n = 7 * (S - 1) - se;
-    const int n1 = n >> 1, n2 = n - n1;
-    RowScale rs;
-    rs.p1 = __uint_as_float((uint32_t)(n1 + 127) << 23);
-    rs.p2 = __uint_as_float((uint32_t)(n2 + 127) << 23);
-    rs.lim = 127 << (7 * (S - 1));
-    return rs;
-}
-
-__device__ __forceinline__ int round_fixed(float x, const RowScale& rs) {
-    const float v = (x * rs.p1) * rs.p2;
-    const int X = (int)__builtin_rintf(v);  // v_rndne_f32: nearest-even; |v| < 2^22 here
-    return min(max(X, -rs.lim), rs.lim);
 }
 
 // Four bytes (low byte of each argument) packed little-endian with v_perm_b32.
@@ -344,9 +335,14 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
     {   // row maxima of this panel's 32 rows, reduced once for the whole block
         const int rr = t & 31, c0 = t >> 5;
         float m = 0.0f;
-        if (r0 + rr < d.R)
-            for (int c = c0; c < d.nch; c += 8)
-                m = fmaxf(m, d.pmax[(size_t)c * rows_total + rp * PANEL_ROWS + rr]);
+        if (r0 + rr < d.R) {
+            const float* pm = d.pmax + rp * PANEL_ROWS + rr;
+            int c = c0;
+            for (; c + 24 < d.nch; c += 32)  // four independent loads in flight
+                m = fmaxf(m, fmaxf(fmaxf(pm[(size_t)c * rows_total], pm[(size_t)(c + 8) * rows_total]),
+                                   fmaxf(pm[(size_t)(c + 16) * rows_total], pm[(size_t)(c + 24) * rows_total])));
+            for (; c < d.nch; c += 8) m = fmaxf(m, pm[(size_t)c * rows_total]);
+        }
         smax[c0][rr] = m;
     }
     __syncthreads();

@@ -86,6 +86,36 @@ def repro_conv2d_grad_input_ws(dy, weight, dx, g, S, workspace, workspace_bytes,
                 stream)
 
 
+# Passes and algorithms of the diagnostic hooks (include/repro_conv.h): AUTO is what the entry
+# points above choose, GEMM the im2col + MFMA GEMM pipeline, DIRECT the one-launch kernels for
+# small filters (forward and input gradient).
+FORWARD, GRAD_WEIGHT, GRAD_INPUT = 0, 1, 2
+ALGO_AUTO, ALGO_GEMM, ALGO_DIRECT = 0, 1, 2
+
+
+def conv2d_algo(pass_, g, S=3):
+    """The algorithm AUTO resolves to for this pass and shape (ALGO_GEMM or ALGO_DIRECT)."""
+    a = ctypes.c_int()
+    c = g.to_c()
+    _check(lib.rg_conv2d_algo(int(pass_), ctypes.byref(c), int(S), ctypes.byref(a)), "conv algo")
+    return a.value
+
+
+def conv2d_algo_workspace(pass_, g, S=3, algo=ALGO_AUTO):
+    n = ctypes.c_size_t()
+    c = g.to_c()
+    _check(lib.rg_conv2d_algo_workspace(int(pass_), ctypes.byref(c), int(S), int(algo),
+                                        ctypes.byref(n)), "conv plan")
+    return n.value
+
+
+def repro_conv2d_algo_ws(pass_, a, b, out, g, S, algo, workspace, workspace_bytes, stream=None):
+    """A pass with its algorithm forced (raw pointers as the entry points above)."""
+    c = g.to_c()
+    return lib.rg_conv2d_algo_ws(int(pass_), a, b, out, ctypes.byref(c), int(S), int(algo),
+                                 workspace, int(workspace_bytes), stream)
+
+
 def _require(t, name):
     import torch
 
@@ -149,6 +179,8 @@ def conv2d_grad_input(dy, w, x_shape, SY, SX, PY, PX, S=3):
                    S, "conv input grad")
 
 
-__all__ = ["ConvShape", "conv2d", "conv2d_grad_input", "conv2d_grad_weight",
+__all__ = ["ALGO_AUTO", "ALGO_DIRECT", "ALGO_GEMM", "FORWARD", "GRAD_INPUT", "GRAD_WEIGHT",
+           "conv2d_algo", "conv2d_algo_workspace", "repro_conv2d_algo_ws",
+           "ConvShape", "conv2d", "conv2d_grad_input", "conv2d_grad_weight",
            "conv2d_grad_input_workspace", "conv2d_grad_weight_workspace", "conv2d_workspace",
            "repro_conv2d_grad_input_ws", "repro_conv2d_grad_weight_ws", "repro_conv2d_ws"]

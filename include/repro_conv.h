@@ -13,7 +13,9 @@
  * position); the input gradient uses one scale per image for dY and one for all weights, so
  * each pixel's terms (several windows, all filters) share a scale. Here all three run on the
  * int8 MFMA contraction of librepro_gemm.so. Output bits depend only on the inputs, the
- * shape and S. Bias is not included (add it; its gradient is rg_sum_fp32_ws).
+ * shape and S. Bias is not included (add it; its gradient is rg_sum_fp32_ws). Small filters
+ * take direct kernels instead (forward and input gradient, at most 2048 products per sum):
+ * one launch, binary64 sums that are exact integers at that length, the same bits.
  *
  * Plain C types only; the stream is a hipStream_t passed as void*. Return values are
  * hipError_t codes (0 success, 1 invalid value, 801 not supported, others from HIP).
@@ -61,6 +63,21 @@ int rg_conv2d_grad_weight_ws(const float* dy, const float* x, float* dw, const r
 int rg_conv2d_grad_input_ws(const float* dy, const float* weight, float* dx,
                             const rg_conv_shape* g, int S, void* workspace,
                             size_t workspace_bytes, void* stream);
+
+/* Diagnostic hooks, with no counterpart in the reference: a pass run with its algorithm
+ * forced, for tests and benchmarks. pass: RG_CONV_FORWARD (a = x, b = weight),
+ * RG_CONV_GRAD_WEIGHT (a = dy, b = x) or RG_CONV_GRAD_INPUT (a = dy, b = weight). algo:
+ * RG_CONV_ALGO_AUTO (the choice of the entry points above), RG_CONV_ALGO_GEMM (im2col and the
+ * int8 MFMA GEMM pipeline) or RG_CONV_ALGO_DIRECT (forward and input gradient only, while one
+ * sum has at most 2048 products and, forward, F*C*KH*KW <= 4096; else 801). Both algorithms
+ * give the same bits. rg_conv2d_algo reports what AUTO resolves to; errors as above, plus 1 for
+ * an unknown pass or algo. */
+enum { RG_CONV_FORWARD = 0, RG_CONV_GRAD_WEIGHT = 1, RG_CONV_GRAD_INPUT = 2 };
+enum { RG_CONV_ALGO_AUTO = 0, RG_CONV_ALGO_GEMM = 1, RG_CONV_ALGO_DIRECT = 2 };
+int rg_conv2d_algo(int pass, const rg_conv_shape* g, int S, int* algo);
+int rg_conv2d_algo_workspace(int pass, const rg_conv_shape* g, int S, int algo, size_t* bytes);
+int rg_conv2d_algo_ws(int pass, const float* a, const float* b, float* out, const rg_conv_shape* g,
+                      int S, int algo, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

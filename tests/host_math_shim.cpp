@@ -4,6 +4,7 @@
 #include <cstdint>
 
 #include "repro_gemm_math.h"
+#include "rg_fastdiv.h"
 
 extern "C" {
 
@@ -35,6 +36,25 @@ void hm_round_to_float_fast_n(const int64_t* T, const int* E, float* out, long l
 
 void hm_round_to_float_f64_n(const int64_t* T, const int* E, float* out, long long n) {
     for (long long i = 0; i < n; ++i) out[i] = repro_gemm::round_to_float_f64(T[i], E[i]);
+}
+
+
+// Pairs (d[i], n[j]) for which the fast divider of the packing kernels differs from n / d, for
+// every i and j; and for one divisor, every n in [n0, n1).
+long long hm_fastdiv_mismatches(const uint32_t* d, long long nd, const uint32_t* n, long long nn) {
+    long long bad = 0;
+    for (long long i = 0; i < nd; ++i) {
+        const rg::FastDiv f = rg::make_fastdiv(d[i]);
+        for (long long j = 0; j < nn; ++j) bad += rg::fdiv(n[j], f) != n[j] / d[i];
+    }
+    return bad;
+}
+
+long long hm_fastdiv_range(uint32_t d, uint32_t n0, uint32_t n1) {
+    const rg::FastDiv f = rg::make_fastdiv(d);
+    long long bad = 0;
+    for (uint32_t n = n0; n < n1; ++n) bad += rg::fdiv(n, f) != n / d;
+    return bad;
 }
 
 }  // extern "C"

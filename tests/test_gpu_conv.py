@@ -87,6 +87,116 @@ def test_conv_wide_dynamic_range(torch_gpu):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), kind
 
 
+RC = rg.repro_conv
+PASSES = {"fwd": RC.FORWARD, "dW": RC.GRAD_WEIGHT, "dX": RC.GRAD_INPUT}
+
+
+def _run_algo(torch, kind, a, b, shape, S, algo):
+    """One pass through the diagnostic hook with its algorithm forced."""
+    N, C, H, W, F, KH, KW = shape[:7]
+    OH, OW = O.conv_out_hw(shape)
+    g = RC.ConvShape(*shape)
+    out_shape = {"fwd": (N, F, OH, OW), "dW": (F, C, KH, KW), "dX": (N, C, H, W)}[kind]
+    out = torch.full(out_shape, float("nan"), dtype=torch.float32, device="cuda")
+    nbytes = RC.conv2d_algo_workspace(PASSES[kind], g, S, algo)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    da, db = to_dev(torch, a), to_dev(torch, b)
+    code = RC.repro_conv2d_algo_ws(PASSES[kind], da.data_ptr(), db.data_ptr(), out.data_ptr(), g,
+                                   S, algo, ws.data_ptr(), ws.numel(),
+                                   torch.cuda.current_stream().cuda_stream)
+    if code != 0:
+        raise rg.ReproGemmError(code, "conv algo")
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+LENET = [(100, 1, 28, 28, 6, 5, 5, 1, 1, 2, 2), (100, 6, 14, 14, 16, 5, 5, 1, 1, 0, 0)]
+# Both algorithms on shapes with strides larger than, equal to and smaller than the kernel,
+# asymmetric padding, 1x1 kernels, planes smaller and larger than a block of 256 pixels, more
+# filters than one pass of accumulators, and the direct kernels' limits: 2048 products per
+# input-gradient sum (128 filters x 4x4) with 6144 staged dY values, 2048 per window and 4096
+# (padded) weights forward.
+DIRECT_SHAPES = SHAPES + [
+    (16, 3, 32, 32, 8, 3, 3, 1, 1, 1, 1), (4, 8, 20, 20, 12, 5, 5, 2, 2, 2, 2),
+    (2, 3, 17, 19, 9, 3, 5, 4, 3, 0, 2), (3, 2, 40, 13, 17, 1, 1, 1, 1, 0, 0),
+    (1, 2, 3, 5, 128, 4, 4, 1, 1, 3, 3), (1, 128, 4, 4, 2, 4, 4, 1, 1, 1, 1),
+] + LENET
+
+
+@pytest.mark.parametrize("S", [1, 2, 3])
+def test_direct_and_gemm_algorithms_match_oracle(torch_gpu, S):
+    """Forward and input gradient by the direct kernels and by the GEMM pipeline, against the
+    oracle bit for bit; the weight gradient (GEMM only) reports not supported for DIRECT."""
+    torch = torch_gpu
+    for shape in DIRECT_SHAPES:
+        if S != 3 and shape in LENET:
+            continue
+        rng = np.random.default_rng(sum(shape) * 5 + S)
+        N, C, H, W, F, KH, KW = shape[:7]
+        OH, OW = O.conv_out_hw(shape)
+        x = (rng.standard_normal(N * C * H * W) *
+             (np.float32(2.0) ** rng.integers(-20, 20, N * C * H * W))).astype(np.float32)
+        x[rng.random(x.size) < 0.1] = 0.0
+        w = (rng.standard_normal(F * C * KH * KW) * 0.1).astype(np.float32)
+        dy = (rng.standard_normal((N, F * OH * OW)) *
+              (np.float32(2.0) ** rng.integers(-30, 30, (N, 1)))).astype(np.float32).reshape(-1)
+        for kind, a, b in (("fwd", x, w), ("dX", dy, w)):
+            want = _oracle(kind, a, b, shape, S).view(np.uint32)
+            for algo in (RC.ALGO_DIRECT, RC.ALGO_GEMM, RC.ALGO_AUTO):
+                note("conv algo", kind, shape, "S=%d algo=%d" % (S, algo))
+                got = _run_algo(torch, kind, a, b, shape, S, algo)
+                assert np.array_equal(got.view(np.uint32), want), (kind, shape, S, algo)
+        g = RC.ConvShape(*shape)
+        with pytest.raises(rg.ReproGemmError):
+            RC.conv2d_algo_workspace(RC.GRAD_WEIGHT, g, S, RC.ALGO_DIRECT)
+
+
+def test_direct_sums_at_their_exactness_limit(torch_gpu):
+    """Every value 127 = 127 * 2^0, which its scale (2^0) maps to the largest fixed-point
+    value X = 127 * 2^14: the central pixel's input-gradient sum has 2048 products of
+    (127 * 2^14)^2 = 2^41.98 each, a forward window sum 2048, so the binary64 sums reach
+    +-2048 * (127 * 2^14)^2, just below 2^53, and must stay exact."""
+    torch = torch_gpu
+    for kind, shape in (("dX", (1, 1, 3, 3, 128, 4, 4, 1, 1, 3, 3)),
+                        ("fwd", (2, 128, 4, 4, 2, 4, 4, 1, 1, 0, 0))):
+        N, C, H, W, F, KH, KW = shape[:7]
+        OH, OW = O.conv_out_hw(shape)
+        x = np.full(N * C * H * W, 127.0, np.float32)
+        dy = np.full(N * F * OH * OW, 127.0, np.float32)
+        for sign in (1.0, -1.0):
+            w = np.full(F * C * KH * KW, sign * 127.0, np.float32)
+            a = x if kind == "fwd" else dy
+            want = _oracle(kind, a, w, shape, 3)
+            assert np.abs(want).max() == np.float32(2048 * 127.0 ** 2)
+            for algo in (RC.ALGO_DIRECT, RC.ALGO_GEMM):
+                note("conv limit", kind, shape, sign, "algo=%d" % algo)
+                got = _run_algo(torch, kind, a, w, shape, 3, algo)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (kind, algo)
+
+
+def test_conv_algorithm_choice(torch_gpu):
+    """Small filters take the direct kernels, large convolutions and the weight gradient the
+    GEMM pipeline; the entry points' workspace is the chosen algorithm's."""
+    for shape in LENET:
+        g = RC.ConvShape(*shape)
+        assert RC.conv2d_algo(RC.FORWARD, g) == RC.ALGO_DIRECT
+        assert RC.conv2d_algo(RC.GRAD_INPUT, g) == RC.ALGO_DIRECT
+        assert RC.conv2d_algo(RC.GRAD_WEIGHT, g) == RC.ALGO_GEMM
+        assert rg.conv2d_workspace(g) == RC.conv2d_algo_workspace(RC.FORWARD, g, 3, RC.ALGO_DIRECT)
+    big = RC.ConvShape(64, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1)
+    for p in (RC.FORWARD, RC.GRAD_WEIGHT, RC.GRAD_INPUT):
+        assert RC.conv2d_algo(p, big) == RC.ALGO_GEMM
+    assert rg.conv2d_grad_input_workspace(big) == RC.conv2d_algo_workspace(
+        RC.GRAD_INPUT, big, 3, RC.ALGO_GEMM)
+    # Beyond the direct kernels' limits: more dY rows than the staging holds (input gradient),
+    # a window of more than 2048 values (forward).
+    with pytest.raises(rg.ReproGemmError):
+        RC.conv2d_algo_workspace(RC.GRAD_INPUT, RC.ConvShape(1, 2, 12, 12, 128, 4, 4, 1, 1, 3, 3),
+                                 3, RC.ALGO_DIRECT)
+    with pytest.raises(rg.ReproGemmError):
+        RC.conv2d_algo_workspace(RC.FORWARD, RC.ConvShape(1, 129, 6, 6, 1, 4, 4), 3, RC.ALGO_DIRECT)
+
+
 def test_conv2d_layer_forward_backward(torch_gpu):
     torch = torch_gpu
     shape = (100, 6, 14, 14, 16, 5, 5, 1, 1, 0, 0)   # LeNet conv2, batch 100

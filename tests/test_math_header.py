@@ -21,7 +21,8 @@ REPO = os.path.dirname(HERE)
 def hm(tmp_path_factory):
     out = str(tmp_path_factory.mktemp("hm") / "libhm.so")
     subprocess.run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
-                    "-fno-fast-math", "-I", os.path.join(REPO, "include"),
+                    "-fno-fast-math", "-I", os.path.join(REPO, "include"), "-I",
+                    os.path.join(REPO, "bit_reproducible_training_amd", "csrc"),
                     os.path.join(HERE, "host_math_shim.cpp"), "-o", out], check=True)
     lib = ctypes.CDLL(out)
     vp, ll = ctypes.c_void_p, ctypes.c_longlong
@@ -32,7 +33,26 @@ def hm(tmp_path_factory):
     lib.hm_round_to_float_f64_n.argtypes = [vp, vp, vp, ll]
     lib.hm_scale_exponent_count_range.argtypes = [ctypes.c_uint32, ctypes.c_uint32, vp]
     lib.hm_scale_exponent_count_range.restype = ll
+    lib.hm_fastdiv_mismatches.argtypes = [vp, ll, vp, ll]
+    lib.hm_fastdiv_mismatches.restype = ll
+    lib.hm_fastdiv_range.argtypes = [ctypes.c_uint32] * 3
+    lib.hm_fastdiv_range.restype = ll
     return lib
+
+
+def test_fastdiv_matches_integer_division(hm):
+    """The packing kernels' multiply-high divider (bit_reproducible_training_amd/csrc/
+    rg_fastdiv.h) against C's unsigned division: every n below 2^31 for two divisors, and
+    divisors 1..4096, powers of two and their neighbours and random ones against edge and
+    random dividends."""
+    assert hm.hm_fastdiv_range(7, 0, 1 << 31) == 0
+    assert hm.hm_fastdiv_range(784, 0, 1 << 31) == 0
+    rng = np.random.default_rng(5)
+    d = np.concatenate([np.arange(1, 4097), [2 ** k + j for k in range(12, 31) for j in (-1, 0, 1)],
+                        rng.integers(1, 2 ** 31, 3000)]).astype(np.uint32)
+    n = np.concatenate([np.arange(0, 70000), 2 ** 31 - 1 - np.arange(0, 1000),
+                        rng.integers(0, 2 ** 31, 20000)]).astype(np.uint32)
+    assert hm.hm_fastdiv_mismatches(d.ctypes.data, d.size, n.ctypes.data, n.size) == 0
 
 
 def test_scale_exponent_exhaustive_vs_oracle(hm):
