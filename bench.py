@@ -393,6 +393,7 @@ def widened(torch, rg, cpu=True, threads=16):
         del x, out, ws
     line["exact_sum"] = sums
     # LeNet-5 convolutions, batch 100 (bench_repro_conv.cu's shapes and input scales).
+    RC = rg.repro_conv
     shapes = [("conv1", rg.ConvShape(100, 1, 28, 28, 6, 5, 5, 1, 1, 2, 2)),
               ("conv2", rg.ConvShape(100, 6, 14, 14, 16, 5, 5))]
     convs, conv_cpu = [], []
@@ -419,6 +420,22 @@ def widened(torch, rg, cpu=True, threads=16):
             row[kind + "_wall_ms"] = round(_wall_ms(torch, run), 4)
             row[kind + "_reference_best_gpu_ms"] = REF_CONV_MS[(name, kind)]
             outs[kind] = o.cpu().numpy().copy()
+            pass_ = {"fwd": RC.FORWARD, "dW": RC.GRAD_WEIGHT, "dX": RC.GRAD_INPUT}[kind]
+            algo = RC.conv2d_algo(pass_, g)
+            row[kind + "_algo"] = "direct" if algo == RC.ALGO_DIRECT else "gemm"
+            if algo == RC.ALGO_DIRECT:  # the GEMM pipeline on the same inputs, for comparison
+                gws = torch.empty(max(RC.conv2d_algo_workspace(pass_, g, 3, RC.ALGO_GEMM), 1),
+                                  dtype=torch.uint8, device="cuda")
+                o2 = torch.empty_like(o)
+
+                def run_gemm():
+                    code = RC.repro_conv2d_algo_ws(pass_, a.data_ptr(), b.data_ptr(), o2.data_ptr(), g,
+                                                   3, RC.ALGO_GEMM, gws.data_ptr(), gws.numel(), stream())
+                    if code != 0:
+                        raise rg.ReproGemmError(code, "conv gemm " + kind)
+
+                row[kind + "_gemm_gpu_ms"] = round(_gpu_ms(torch, run_gemm), 4)
+                row[kind + "_gemm_same_bits"] = bool(torch.equal(o2.view(torch.int32), o.view(torch.int32)))
         convs.append(row)
         conv_cpu.append((name, g.astuple(), [("fwd", x.cpu().numpy(), w.cpu().numpy()),
                                              ("dW", dy.cpu().numpy(), x.cpu().numpy()),

@@ -513,9 +513,15 @@ PlanExtras conv_extras(bool raw) {
 // Direct kernels' shape limits (exactness of the binary64 sums, LDS for the weights) and the
 // automatic choice: direct while the multiply-adds and the blocks' redundant reads of weights
 // and maxima stay small (at most about 20 us of work on MI355X), where the GEMM pipeline's
-// launches, padding of K to 64 and packed copies cost more than the arithmetic.
+// launches, padding of K to 64 and packed copies cost more than the arithmetic, and while one
+// thread's chain of multiply-adds stays short: the direct kernels' time grows with it (MI355X,
+// LeNet-5 at batch 100: forward 11 us at 200 per thread against 33 us for the GEMM pipeline,
+// 28 us at 1200 against 23 us; input gradient 15 us at 150 and 26 us at 400 against 53 and
+// 41 us).
 constexpr double DIRECT_AUTO_MACS = 268435456.0;  // 2^28
 constexpr double DIRECT_AUTO_READS = 67108864.0;  // 2^26
+constexpr long long FWD_AUTO_CHAIN = 512;         // K * (padded F) / G multiply-adds per thread
+constexpr long long DX_AUTO_CHAIN = 768;          // F * KH * KW
 
 // Direct tilings (see the kernels): forward blocks of THREADS / G windows of one image, input
 // gradient blocks of THREADS pixels of one plane; the LDS each needs for its staged rows is
@@ -565,10 +571,12 @@ bool direct_preferred(Kind kind, const Geom& g) {
     if (!direct_possible(kind, g)) return false;
     double macs, reads;
     if (kind == Kind::Forward) {
+        if ((long long)g.K * fwd_padded_filters(g.F) / fwd_groups(g.F) > FWD_AUTO_CHAIN) return false;
         const double blocks = (double)g.N * fwd_tiles_per_image(g);
         macs = (double)g.windows * g.F * g.K;
         reads = blocks * ((double)g.F * g.K + (double)fwd_patch_floats(g));
     } else {
+        if ((long long)g.F * g.KH * g.KW > DX_AUTO_CHAIN) return false;
         const double blocks = (double)g.N * g.C * dx_tiles_per_plane(g);
         macs = (double)g.N * g.C * g.H * g.W * g.F * g.KH * g.KW;
         reads = blocks * ((double)g.F * g.P + (double)g.F * g.C * g.KH * g.KW);

@@ -175,14 +175,19 @@ def test_direct_sums_at_their_exactness_limit(torch_gpu):
 
 
 def test_conv_algorithm_choice(torch_gpu):
-    """Small filters take the direct kernels, large convolutions and the weight gradient the
-    GEMM pipeline; the entry points' workspace is the chosen algorithm's."""
-    for shape in LENET:
-        g = RC.ConvShape(*shape)
-        assert RC.conv2d_algo(RC.FORWARD, g) == RC.ALGO_DIRECT
-        assert RC.conv2d_algo(RC.GRAD_INPUT, g) == RC.ALGO_DIRECT
+    """Small filters take the direct kernels (LeNet conv1 both passes, conv2's input gradient;
+    conv2's forward, 1200 multiply-adds per thread, the GEMM pipeline), large convolutions and
+    the weight gradient the GEMM pipeline; the entry points' workspace is the chosen
+    algorithm's."""
+    conv1, conv2 = (RC.ConvShape(*s) for s in LENET)
+    want = {(0, RC.FORWARD): RC.ALGO_DIRECT, (0, RC.GRAD_INPUT): RC.ALGO_DIRECT,
+            (1, RC.FORWARD): RC.ALGO_GEMM, (1, RC.GRAD_INPUT): RC.ALGO_DIRECT}
+    for i, g in enumerate((conv1, conv2)):
+        for p in (RC.FORWARD, RC.GRAD_INPUT):
+            assert RC.conv2d_algo(p, g) == want[(i, p)], (i, p)
         assert RC.conv2d_algo(RC.GRAD_WEIGHT, g) == RC.ALGO_GEMM
-        assert rg.conv2d_workspace(g) == RC.conv2d_algo_workspace(RC.FORWARD, g, 3, RC.ALGO_DIRECT)
+    assert rg.conv2d_workspace(conv1) == RC.conv2d_algo_workspace(RC.FORWARD, conv1, 3, RC.ALGO_DIRECT)
+    assert rg.conv2d_workspace(conv2) == RC.conv2d_algo_workspace(RC.FORWARD, conv2, 3, RC.ALGO_GEMM)
     big = RC.ConvShape(64, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1)
     for p in (RC.FORWARD, RC.GRAD_WEIGHT, RC.GRAD_INPUT):
         assert RC.conv2d_algo(p, big) == RC.ALGO_GEMM
