@@ -478,6 +478,87 @@ def widened(torch, rg, cpu=True, threads=16):
     print(json.dumps(line), flush=True)
 
 
+# BASELINE configurations 2, 3 and 5 (configuration 1 is 256^3 and 4 the default line's
+# adversarial run): shapes, transposes, slices and value scales of tests/golden/configs.py,
+# which the GPU tests check against the CPU oracle's hashes. Here: (name, M, N, K, ta, tb, S,
+# scale of A, scale of B) with inputs drawn on the GPU (torch.randn, uniform for LeNet weights).
+def _config_cases():
+    cases = []
+    for li, (fin, fout) in enumerate([(400, 120), (120, 84), (84, 10)]):
+        u = 1.0 / (fin ** 0.5)
+        for S in (1, 2, 3):
+            tag = "c2.fc%d.%dx%d" % (li + 1, fin, fout)
+            cases += [(tag + ".fwd.S%d" % S, 64, fout, fin, 0, 1, S, 1.0, -u),
+                      (tag + ".dX.S%d" % S, 64, fin, fout, 0, 0, S, 1.0, -u),
+                      (tag + ".dW.S%d" % S, fout, fin, 64, 1, 0, S, 1.0, 1.0)]
+    for nm, fin, fout in [("qkv", 768, 2304), ("attn_proj", 768, 768), ("mlp_fc", 768, 3072),
+                          ("mlp_proj", 3072, 768)]:
+        tag = "c3." + nm
+        cases += [(tag + ".fwd", 8192, fout, fin, 0, 1, 3, 1.0, 0.02),
+                  (tag + ".dX", 8192, fin, fout, 0, 0, 3, 1.0, 0.02),
+                  (tag + ".dW", fout, fin, 8192, 1, 0, 3, 1.0, 1.0)]
+    cases += [("c5.lm_head.fwd", 8192, 50257, 768, 0, 1, 3, 1.0, 1.0),
+              ("c5.lm_head.dW", 50257, 768, 8192, 1, 0, 3, 1.0, 1.0),
+              ("c5.tall_skinny", 1024, 1024, 65536, 0, 0, 3, 1.0, 1.0)]
+    return cases
+
+
+def configs_mode(torch, rg, reps=10, warmup=3):
+    """One JSON line: every GEMM of BASELINE configurations 2, 3 and 5 timed on the GPU (HIP
+    events around `reps` back-to-back GEMMs after `warmup`), its effective FP32 TFLOP/s, the
+    contraction's share of the dense int8 MFMA peak (stage events, a second pass), the plan,
+    and whether two runs gave identical bits."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2024)
+    sp = torch.cuda.current_stream().cuda_stream
+    rows = []
+    for name, M, N, K, ta, tb, S, sa, sb in _config_cases():
+        def draw(n, scale):
+            if scale < 0:  # U(-|scale|, |scale|)
+                return (torch.rand(n, device="cuda", generator=gen) * 2 - 1) * -scale
+            return torch.randn(n, device="cuda", generator=gen) * scale
+        dA, dB = draw(M * K, sa), draw(K * N, sb)
+        cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb)
+        plan = rg.make_plan(M, N, K, cfg)
+        ws = torch.empty(max(plan.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
+        C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+
+        def step(events=None):
+            code = rg.repro_gemm_fp32_ws(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), M, N, K, cfg,
+                                         ws.data_ptr(), ws.numel(), sp, events)
+            if code != 0:
+                raise rg.ReproGemmError(code, name)
+
+        for _ in range(warmup):
+            step()
+        first = C.clone()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        for e in evs:
+            e.record()
+        torch.cuda.synchronize()
+        step([e.cuda_event for e in evs])
+        torch.cuda.synchronize()
+        contract_ms = evs[1].elapsed_time(evs[2])
+        flops = 2.0 * M * N * K
+        rows.append({"case": name, "M": M, "N": N, "K": K, "ta": ta, "tb": tb, "S": S,
+                     "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "contract_ms": round(contract_ms, 4),
+                     "contract_int8_frac": round(S * S * flops / (contract_ms * 1e-3) / (PEAK_INT8_TOPS * 1e12), 4),
+                     "plan": "%dx%d split %d" % (plan.tile_m, plan.tile_n, plan.split_k),
+                     "repeat_bits_equal": bool(torch.equal(first.view(torch.int32), C.view(torch.int32)))})
+        del dA, dB, ws, C, first
+        torch.cuda.empty_cache()
+    print(json.dumps({"mode": "configs", "data": "synthetic (torch.randn / uniform on the GPU, seed 2024)",
+                      "cases": rows}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -492,6 +573,8 @@ def main():
                     help="time the exact sum, convolutions, batched GEMM and Linear layer instead")
     ap.add_argument("--suite", action="store_true",
                     help="time the reference GPT-2 suite's 21 GEMMs (1024 tokens) instead")
+    ap.add_argument("--configs", action="store_true",
+                    help="time every GEMM of BASELINE configurations 2, 3 and 5 instead")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 device-to-device copies of 256 MiB (a plain copy kernel of "
                          "known size, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -508,6 +591,9 @@ def main():
 
     if args.suite:
         suite(torch, rg)
+        return
+    if args.configs:
+        configs_mode(torch, rg)
         return
     if args.widened:
         widened(torch, rg, cpu=not args.no_cpu, threads=args.cpu_threads)
