@@ -580,8 +580,9 @@ def main():
                          "known size, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the reproducible GEMM shards without changing bits; see DESIGN.md).",
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the "
+              "reproducible GEMM would shard along M or N with no exchange, or along K with "
+              "one exact int64 all-reduce, without changing bits).",
               file=sys.stderr)
         sys.exit(2)
 
