@@ -102,3 +102,56 @@ def test_batched_and_sum_replays_equal_eager(torch_gpu):
         torch.cuda.synchronize()
         assert np.array_equal(_bits(scores), want_s), rep
         assert np.array_equal(_bits(bias_grad), want_b), rep
+
+
+def test_conv_replays_equal_eager(torch_gpu):
+    """The three convolution passes of LeNet conv1 in one graph: the forward and the input
+    gradient take the direct kernels, the weight gradient the GEMM pipeline (im2col, slicing,
+    split-K contraction, parallel reduction)."""
+    torch = torch_gpu
+    RC = rg.repro_conv
+    shape = (100, 1, 28, 28, 6, 5, 5, 1, 1, 2, 2)
+    g_ = RC.ConvShape(*shape)
+    assert RC.conv2d_algo(RC.FORWARD, g_) == RC.ALGO_DIRECT
+    assert RC.conv2d_algo(RC.GRAD_INPUT, g_) == RC.ALGO_DIRECT
+    torch.manual_seed(3)
+    x = torch.randn(g_.N, g_.C, g_.H, g_.W, device="cuda")
+    w = 0.1 * torch.randn(g_.F, g_.C, g_.KH, g_.KW, device="cuda")
+    dy = 1e-3 * torch.randn(g_.N, g_.F, g_.OH, g_.OW, device="cuda")
+    y, dw, dx = torch.empty_like(dy), torch.empty_like(w), torch.empty_like(x)
+    passes = [(rg.repro_conv2d_ws, rg.conv2d_workspace(g_), x, w, y),
+              (rg.repro_conv2d_grad_weight_ws, rg.conv2d_grad_weight_workspace(g_), dy, x, dw),
+              (rg.repro_conv2d_grad_input_ws, rg.conv2d_grad_input_workspace(g_), dy, w, dx)]
+    wss = [torch.empty(max(n, 1), dtype=torch.uint8, device="cuda") for _, n, _, _, _ in passes]
+
+    def call():
+        for (fn, _, a, b, o), ws in zip(passes, wss):
+            code = fn(a.data_ptr(), b.data_ptr(), o.data_ptr(), g_, 3, ws.data_ptr(), ws.numel(),
+                      torch.cuda.current_stream().cuda_stream)
+            assert code == 0
+
+    def want():
+        xn, wn, dyn = (t.cpu().numpy().reshape(-1) for t in (x, w, dy))
+        return [O.conv2d(xn, wn, shape, 3).view(np.uint32),
+                O.conv2d_grad_weight(dyn, xn, shape, 3).view(np.uint32),
+                O.conv2d_grad_input(dyn, wn, shape, 3).view(np.uint32)]
+
+    note("graph conv passes")
+    g = _capture(torch, call)
+    w1 = want()
+    for rep in range(3):
+        for o in (y, dw, dx):
+            o.fill_(float("nan"))
+        for ws in wss:
+            ws.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, exp in zip((y, dw, dx), w1):
+            assert np.array_equal(_bits(o).reshape(-1), exp.reshape(-1)), rep
+    x.copy_(torch.randn(g_.N, g_.C, g_.H, g_.W, device="cuda") * 7.0)
+    dy.copy_(torch.randn(g_.N, g_.F, g_.OH, g_.OW, device="cuda"))
+    g.replay()
+    torch.cuda.synchronize()
+    for o, exp in zip((y, dw, dx), want()):
+        assert np.array_equal(_bits(o).reshape(-1), exp.reshape(-1))
