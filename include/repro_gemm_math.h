@@ -11,13 +11,23 @@
 // IEEE host compiler provide it. round_to_float_f64, the faster equivalent of round_to_float
 // used by the GPU epilogues, relies on exact binary64 arithmetic and one IEEE conversion to
 // binary32. Do not build with -ffast-math or denormal flushing.
+#include <cmath>
 #include <cstdint>
+#include <cstring>
 
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
 #define RG_HD __host__ __device__
 #else
 #define RG_HD
+// Host-only builds of code written for both sides (repro_conv_math.cuh marks its functions
+// __host__ __device__) see the qualifiers as nothing, as under the reference's header.
+#ifndef __host__
+#define __host__
+#endif
+#ifndef __device__
+#define __device__
+#endif
 #endif
 
 namespace repro_gemm {
