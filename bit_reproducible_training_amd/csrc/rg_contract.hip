@@ -159,6 +159,19 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     }
     const uint32_t voff = (uint32_t)lane * 16u;
 
+    // The tile's exponents, loaded before the pipeline so that the epilogue does not wait for
+    // them: lane L holds row L % (32 WTI) of this wavefront's rows (the epilogue takes each
+    // row's exponent from its lane with a shuffle) and the exponents of its own columns. The
+    // arrays cover the padded rows and columns, so the loads need no bounds check.
+    const int e0 = -14 * (S - 1);
+    int er_lane = 0;
+    int ec[WTJ];
+    if (partial == nullptr) {
+        er_lane = eA[tm * BM + wm * WTI * 32 + lane % (WTI * 32)];
+#pragma unroll
+        for (int tj = 0; tj < WTJ; ++tj) ec[tj] = eB[tn * BN + (wn * WTJ + tj) * 32 + (lane & 31)] + e0;
+    }
+
     v16i acc[L][WTI][WTJ];
 #pragma unroll
     for (int l = 0; l < L; ++l)
@@ -302,9 +315,7 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     if (s0 < s1) tail();
 
     // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
-    // column lane%32. The exponent arrays cover the padded rows and columns, so their loads
-    // need no bounds check and are issued together before any arithmetic.
-    const int e0 = -14 * (S - 1);
+    // column lane%32.
     const int row0 = tm * BM + wm * WTI * 32 + 4 * (lane >> 5);
     const bool rows_inside = tm * BM + BM <= M;  // uniform: no row of the block is past M
     int col[WTJ];
@@ -312,14 +323,12 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     for (int tj = 0; tj < WTJ; ++tj) col[tj] = tn * BN + (wn * WTJ + tj) * 32 + (lane & 31);
     if (partial == nullptr) {
         const bool inside = rows_inside && tn * BN + BN <= N;  // uniform: the whole block tile
-        int ec[WTJ];
-#pragma unroll
-        for (int tj = 0; tj < WTJ; ++tj) ec[tj] = eB[col[tj]] + e0;
 #pragma unroll
         for (int ti = 0; ti < WTI; ++ti) {
             int er[16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) er[e] = eA[row0 + ti * 32 + 8 * (e >> 2) + (e & 3)];
+            for (int e = 0; e < 16; ++e)
+                er[e] = __shfl(er_lane, ti * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), 64);
 #pragma unroll
             for (int tj = 0; tj < WTJ; ++tj) {
                 float* cp = C + (size_t)(row0 + ti * 32) * ldc + col[tj];
