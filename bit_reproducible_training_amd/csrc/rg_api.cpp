@@ -299,11 +299,20 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
         d.pmax = pm;
         d.out = out;
         d.expo = expo;
+        d.im2col = 0;
+        std::memset(&d.g, 0, sizeof d.g);
         slice_grid(d);
         return d;
     };
-    const SliceDesc da = desc(A, L.M, L.Mp, L.a_strided, addr.lda, addr.stride_a, L.nch_a,
-                              L.kch_a, pma, qa, ea);
+    SliceDesc da = desc(A, L.M, L.Mp, L.a_strided, addr.lda, addr.stride_a, L.nch_a,
+                        L.kch_a, pma, qa, ea);
+    if (opt.im2col_a) {  // op(A) gathered: only the one-pass route reads through Im2col
+        if (i32 || L.batch != 1 || L.a_strided || opt.group_a > 0 || !onepass_eligible(da))
+            return hipErrorInvalidValue;
+        da.im2col = 1;
+        da.g = *opt.im2col_a;
+        da.vec = 0;
+    }
     const SliceDesc db = desc(B, L.N, L.Np, L.b_strided, addr.ldb, addr.stride_b, L.nch_b,
                               L.kch_b, pmb, qb, eb);
     const OutAddr out{addr.ldc, addr.stride_c};
@@ -315,6 +324,15 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     const bool one_b = !i32 && opt.group_b == 0 && onepass_eligible(db);
     if (one_a && one_b) {
         launch_onepass(da, true, db, true, L.S, stream);
+    } else if (da.im2col) {
+        // the gathering operand on its own, then op(B)'s two passes
+        launch_onepass(da, true, db, false, L.S, stream);
+        SliceDesc none = da;
+        none.max_blocks = 0;
+        none.split_blocks = 0;
+        launch_absmax(none, db, stream);
+        if (opt.group_b > 0) launch_group_max(db, opt.group_b, stream);
+        launch_split(none, db, L.S, i32, stream);
     } else if (one_a != one_b) {
         // one launch for the one-pass operand and the other's maxima, then the other's split
         const SliceDesc& one = one_a ? da : db;

@@ -587,6 +587,7 @@ bool direct_preferred(Kind kind, const Geom& g) {
 struct ConvPlan {
     Geom g;
     bool direct;
+    bool implicit;   // forward GEMM reads the im2col matrix through Im2col (no cols buffer)
     Layout L;        // the GEMM (GEMM algorithm only)
     size_t buf0, buf1, gemm, total;
 };
@@ -621,8 +622,11 @@ int conv_plan(Kind kind, const rg_conv_shape* s, int S, int algo, ConvPlan* P) {
         case Kind::Forward:       // C[W][F] = cols[W][K] * weight[F][K]^T
             cfg.trans_b = 1;
             e = layout_for_current_device(W, g.F, g.K, &cfg, &p.L, conv_extras(false));
-            b0 = (size_t)W * g.K * sizeof(float);   // cols
-            b1 = (size_t)W * g.F * sizeof(float);   // Y rows
+            // The one-pass slicing gathers cols from x itself (implicit im2col); longer
+            // windows take the two passes over a packed cols matrix.
+            p.implicit = e == hipSuccess && p.L.Kp <= ONEPASS_MAX_K;
+            b0 = p.implicit ? 0 : (size_t)W * g.K * sizeof(float);   // cols
+            b1 = (size_t)W * g.F * sizeof(float);                     // Y rows
             break;
         case Kind::GradWeight:    // dW[F][K] = (dY rows[W][F])^T * cols[W][K]
             cfg.trans_a = 1;
@@ -693,11 +697,23 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
     const size_t outn = (size_t)g.windows * g.F;
     switch (kind) {
         case Kind::Forward: {
-            float* cols = reinterpret_cast<float*>(base + p.buf0);
             float* yrows = reinterpret_cast<float*>(base + p.buf1);
-            launch_im2col(a, cols, g, stream);
-            e = gemm_launch(cols, b, yrows, p.L, gws, stream, nullptr, GemmOptions(),
-                            dense_addressing(p.L));
+            if (p.implicit) {
+                Im2col ic;
+                ic.x = a;
+                ic.C = g.C; ic.H = g.H; ic.W = g.W; ic.KH = g.KH; ic.KW = g.KW;
+                ic.SY = g.SY; ic.SX = g.SX; ic.PY = g.PY; ic.PX = g.PX; ic.OW = g.OW; ic.P = g.P;
+                ic.dP = g.dP; ic.dOW = g.dOW; ic.dKHW = g.dKHW; ic.dKW = g.dKW;
+                GemmOptions opt;
+                opt.im2col_a = &ic;
+                e = gemm_launch(nullptr, b, yrows, p.L, gws, stream, nullptr, opt,
+                                dense_addressing(p.L));
+            } else {
+                float* cols = reinterpret_cast<float*>(base + p.buf0);
+                launch_im2col(a, cols, g, stream);
+                e = gemm_launch(cols, b, yrows, p.L, gws, stream, nullptr, GemmOptions(),
+                                dense_addressing(p.L));
+            }
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL(rows_to_nfp_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
                                stream, yrows, out, g);

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "repro_gemm.h"
+#include "rg_fastdiv.h"
 
 #include <cstddef>
 #include <cstdint>
@@ -102,6 +103,15 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
                 bool ta, bool tb, const DeviceInfo& dev, Layout* L,
                 const PlanExtras& extras = PlanExtras());
 
+// Implicit im2col: the operand's row w = (n, oy, ox) is window (oy, ox) of image n of
+// x[N][C][H][W] (P = OH * OW windows per image), its element k = (c, ky, kx) the input value
+// at (c, oy * SY - PY + ky, ox * SX - PX + kx), zero in the padding.
+struct Im2col {
+    const float* x;
+    int C, H, W, KH, KW, SY, SX, PY, PX, OW, P;
+    FastDiv dP, dOW, dKHW, dKW;
+};
+
 // One operand of the slice split: `batch` items, each op(X) of R rows of K values, item b at
 // src + b * bstride. Element (r, k) of an item is at [r * ld + k] (row access), or at
 // [k * ld + r] when `strided` (row r read along k with stride ld). Rows are stacked item by
@@ -120,6 +130,8 @@ struct SliceDesc {
     void* out;          // digit panels (or int32 [batch * Rp][Kp] for the reference algorithm)
     int* expo;          // [batch * Rp] exponents
     long long max_blocks, split_blocks;
+    int im2col;         // rows are gathered through `g` (one-pass route, row access, one item)
+    Im2col g;
 };
 
 // Fills max_blocks / split_blocks of d.
@@ -146,6 +158,10 @@ struct GemmOptions {
     int group_a = 0;
     int group_b = 0;
     bool raw = false;
+    // op(A) gathered from an image tensor instead of read from A (the convolution's forward
+    // pass on the implicit im2col matrix); needs the one-pass route (padded K <= ONEPASS_MAX_K,
+    // no group scales, one item).
+    const Im2col* im2col_a = nullptr;
 };
 
 // Layout for the current device (queried once per device and cached).

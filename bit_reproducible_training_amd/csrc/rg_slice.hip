@@ -411,7 +411,26 @@ __global__ void __launch_bounds__(256) split_kernel(SliceDesc a, SliceDesc b) {
 // Wave-strip form (WS, padded K <= 256, NF4 = its k-panels): each wavefront owns its own strip
 // (strip 8 blk + w) over all of K, so short rows keep all 8 wavefronts busy; the maxima are
 // then reduced within the wavefront only and no block barrier is needed.
-template <int S, int NF4, bool WS = false>
+// Four consecutive values k .. k+3 (those below K) of row `row` of the implicit im2col matrix
+// whose window origin in image xn is (y0, x0); zero in the padding and past K.
+__device__ __forceinline__ float4 im2col_values(const Im2col& g, const float* xn, int y0, int x0,
+                                                int k, int K) {
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        t[j] = 0.0f;
+        const int kk = k + j;
+        if (kk < K) {
+            const int c = (int)fdiv((uint32_t)kk, g.dKHW), r = kk - c * (g.KH * g.KW);
+            const int ky = (int)fdiv((uint32_t)r, g.dKW), kx = r - ky * g.KW;
+            const int y = y0 + ky, x = x0 + kx;
+            if (y >= 0 && y < g.H && x >= 0 && x < g.W) t[j] = xn[((size_t)c * g.H + y) * g.W + x];
+        }
+    }
+    return make_float4(t[0], t[1], t[2], t[3]);
+}
+
+template <int S, int NF4, bool WS = false, bool G = false>
 __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][8];
     __shared__ int sse[8];
@@ -430,7 +449,32 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     const int npk = d.Kp / PANEL_K;
     float4 v[NF4];
     float wmax = 0.0f;
-    if (!d.strided) {
+    if (G && d.im2col) {  // rows of the implicit im2col matrix (one item, row access)
+        const int row = r0 + (lane >> 3);
+        const Im2col& g = d.g;
+        int y0 = 0, x0 = 0;
+        const float* xn = g.x;
+        if (row < d.R) {
+            const int n = (int)fdiv((uint32_t)row, g.dP), p = row - n * g.P;
+            const int oy = (int)fdiv((uint32_t)p, g.dOW), ox = p - oy * g.OW;
+            y0 = oy * g.SY - g.PY;
+            x0 = ox * g.SX - g.PX;
+            xn = g.x + (size_t)n * g.C * g.H * g.W;
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NF4; ++i) {
+            const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
+            v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (row < d.R && k < d.K) v[i] = im2col_values(g, xn, y0, x0, k, d.K);
+        }
+#pragma unroll
+        for (int i = 0; i < NF4; ++i) m = fmaxf(m, max4(v[i]));
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        if (WS) wmax = m;  // lanes 8j..8j+7 all hold row j's maximum
+        else if ((lane & 7) == 0) smax[w][lane >> 3] = m;
+    } else if (!d.strided) {
         const int row = r0 + (lane >> 3);
         float m = 0.0f;
 #pragma unroll
@@ -561,11 +605,11 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     }
 }
 
-template <int S, int NF4, bool WS>
+template <int S, int NF4, bool WS, bool G>
 __global__ void __launch_bounds__(512) slice_onepass_kernel(SliceDesc a, SliceDesc b, long long a_blocks) {
     const long long blk = blockIdx.x;
-    if (blk < a_blocks) slice_onepass<S, NF4, WS>(a, blk);
-    else slice_onepass<S, NF4, WS>(b, blk - a_blocks);
+    if (blk < a_blocks) slice_onepass<S, NF4, WS, G>(a, blk);
+    else slice_onepass<S, NF4, WS, G>(b, blk - a_blocks);
 }
 
 // The one pass of operand `one` fused with the partial maxima (first of the two passes) of
@@ -600,13 +644,18 @@ bool onepass_eligible(const SliceDesc& d) {
 void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
                     hipStream_t stream) {
     const int kp = use_a ? a.Kp : b.Kp;
+    // Gathering (implicit im2col) instantiations only when an operand gathers, so the plain
+    // GEMM's kernels carry none of that code.
+    const bool gather = (use_a && a.im2col) || (use_b && b.im2col);
     if (kp <= 256) {  // wave strips: 8 strips per block
         const long long na = use_a ? ((long long)a.batch * (a.Rp / 8) + 7) / 8 : 0;
         const long long nb = use_b ? ((long long)b.batch * (b.Rp / 8) + 7) / 8 : 0;
         if (na + nb == 0) return;
         const unsigned blocks = (unsigned)(na + nb);
         const int nf4 = kp <= 64 ? 2 : (kp <= 128 ? 4 : 8);
-#define RG_ONEPASS_WS(SS, NF) slice_onepass_kernel<SS, NF, true><<<blocks, 512, 0, stream>>>(a, b, na)
+#define RG_ONEPASS_WS(SS, NF)                                                                  \
+    (gather ? slice_onepass_kernel<SS, NF, true, true><<<blocks, 512, 0, stream>>>(a, b, na)  \
+            : slice_onepass_kernel<SS, NF, true, false><<<blocks, 512, 0, stream>>>(a, b, na))
         switch (S * 100 + nf4) {
             case 102: RG_ONEPASS_WS(1, 2); break;
             case 104: RG_ONEPASS_WS(1, 4); break;
@@ -627,7 +676,9 @@ void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use
     if (na + nb == 0) return;
     const unsigned blocks = (unsigned)(na + nb);
     const int nf4 = kp <= 1024 ? 4 : (kp <= 2048 ? 8 : 16);
-#define RG_ONEPASS(SS, NF) slice_onepass_kernel<SS, NF, false><<<blocks, 512, 0, stream>>>(a, b, na)
+#define RG_ONEPASS(SS, NF)                                                                      \
+    (gather ? slice_onepass_kernel<SS, NF, false, true><<<blocks, 512, 0, stream>>>(a, b, na)    \
+            : slice_onepass_kernel<SS, NF, false, false><<<blocks, 512, 0, stream>>>(a, b, na))
     switch (S * 100 + nf4) {
         case 104: RG_ONEPASS(1, 4); break;
         case 108: RG_ONEPASS(1, 8); break;
