@@ -44,9 +44,10 @@ int max_steps_per_part(int S) {
 
 // Row-max pass chunking, from shapes only (so the workspace size never depends on pointer
 // alignment): enough blocks to keep HBM busy, at most 16 (row access) or 32 (column access)
-// partial maxima per row, chunk lengths a multiple of 4 for float4 loads. A column-access
-// operand of at most 32 columns per item (read as whole rows, few blocks per chunk) takes up
-// to 256 chunks of at least 256 k. R is the item's row count, rows all items' rows.
+// partial maxima per row, chunk lengths a multiple of 4 for float4 loads. Column-access
+// operands of at most 32 columns per item (read as whole rows, few blocks per chunk), and long
+// columns over few column groups, take up to 256 chunks of at least 256 k. R is the item's
+// row count, rows all items' rows.
 void choose_chunks(int R, int rows, int K, bool strided, int* nch, int* kch) {
     int n;
     if (strided && R <= 32) {
@@ -54,6 +55,9 @@ void choose_chunks(int R, int rows, int K, bool strided, int* nch, int* kch) {
     } else if (strided) {
         int groups = ceil_div(rows, rows % 4 == 0 ? 256 : 64);
         n = std::min(ceil_div(1024, groups), std::min(32, ceil_div(K, 16)));
+        // A long K over few column groups (a convolution's weight gradient: 576 positions
+        // over 100352 windows) needs more chunks to give the pass enough blocks.
+        n = std::max(n, std::min(ceil_div(1024, groups), std::min(256, ceil_div(K, 256))));
     } else {
         n = std::min(ceil_div(2048, rows), std::min(16, ceil_div(K, 256)));
     }

@@ -7,6 +7,7 @@
 //   input grad   dX[pixel] = sum over the (window, position) pairs that read the pixel of
 //                T[w][k] = sum_f D[w][f] * Wq[f][k]            one scale per image of dY,
 //                                                              one for all weights
+//                (computed as the GEMM of T^T = Wq^T D^T, stored [k][w])
 // The first two are exactly the reproducible GEMM on the im2col matrix, so they run the GEMM
 // pipeline on packed operands. The input gradient runs the same slicing and contraction with
 // group scales (every window of an image shares the image's scale; all positions share the
@@ -127,13 +128,15 @@ __device__ __forceinline__ int window_at(int v, int pad, int k, const FastDiv& d
 }
 
 // dX[n][c][y][x]: the exact int64 sum of T[w][k] (summed over the split parts) over every
-// window w that reads pixel (y, x) at position k = (c, ky, kx), rounded once.
+// window w that reads pixel (y, x) at position k = (c, ky, kx), rounded once. T is stored
+// transposed, [k][w]: for one (ky, kx) the threads of a pixel row read consecutive windows.
+// ea: the positions' exponents (all the weights' one), eb: the windows' (their image's).
 __global__ void __launch_bounds__(THREADS)
 col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __restrict__ ea,
                     const int* __restrict__ eb, float* __restrict__ dx, Geom g, int e0) {
     const uint32_t total = (uint32_t)((long long)g.N * g.C * g.H * g.W);
     const size_t MN = (size_t)g.windows * g.K;
-    const int eW = eb[0];
+    const int eW = ea[0];
     for (uint32_t i = blockIdx.x * THREADS + threadIdx.x; i < total; i += gridDim.x * THREADS) {
         const uint32_t q1 = fdiv(i, g.dW);
         const int xx = (int)(i - q1 * (uint32_t)g.W);
@@ -149,11 +152,11 @@ col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __re
                 const int ox = window_at(xx, g.PX, kx, g.dSX, g.SX, g.OW);
                 if (ox < 0) continue;
                 const size_t w = (size_t)n * g.P + (size_t)oy * g.OW + ox;
-                const size_t at = w * g.K + ((size_t)c * g.KH + ky) * g.KW + kx;
+                const size_t at = (((size_t)c * g.KH + ky) * g.KW + kx) * g.windows + w;
                 for (int s = 0; s < split; ++s) t += part[(size_t)s * MN + at];
             }
         }
-        dx[i] = repro_gemm::round_to_float_fast(t, ea[(size_t)n * g.P] + eW + e0);
+        dx[i] = repro_gemm::round_to_float_fast(t, eb[(size_t)n * g.P] + eW + e0);
     }
 }
 
@@ -634,8 +637,12 @@ int conv_plan(Kind kind, const rg_conv_shape* s, int S, int algo, ConvPlan* P) {
             b0 = (size_t)W * g.F * sizeof(float);   // dY rows
             b1 = (size_t)W * g.K * sizeof(float);   // cols
             break;
-        case Kind::GradInput:     // T[W][K] = dY rows[W][F] * weight[F][K], exact int64
-            e = layout_for_current_device(W, g.K, g.F, &cfg, &p.L, conv_extras(true));
+        case Kind::GradInput:     // T^T[K][W] = weight^T[K][F] * (dY rows[W][F])^T, exact int64
+            // Transposed, so that the pixels of one row read neighbouring windows of one
+            // position k in col2im_round (consecutive addresses).
+            cfg.trans_a = 1;
+            cfg.trans_b = 1;
+            e = layout_for_current_device(g.K, W, g.F, &cfg, &p.L, conv_extras(true));
             b0 = (size_t)W * g.F * sizeof(float);   // dY rows
             break;
     }
@@ -735,10 +742,10 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
             hipLaunchKernelGGL(nfp_to_rows_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
                                stream, a, dyrows, g);
             GemmOptions opt;
-            opt.group_a = g.P;   // one scale per image
-            opt.group_b = g.K;   // one scale for all weights
+            opt.group_a = g.K;   // rows of op(A) are the positions: one scale for all weights
+            opt.group_b = g.P;   // rows of op(B)^T are the windows: one scale per image
             opt.raw = true;
-            e = gemm_launch(dyrows, b, nullptr, p.L, gws, stream, nullptr, opt,
+            e = gemm_launch(b, dyrows, nullptr, p.L, gws, stream, nullptr, opt,
                             dense_addressing(p.L));
             if (e != hipSuccess) return e;
             const size_t pixels = (size_t)g.N * g.C * g.H * g.W;
