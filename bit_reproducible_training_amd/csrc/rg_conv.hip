@@ -94,6 +94,29 @@ im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uin
     }
 }
 
+// dst[b][c][r] = src[b][r][c] for `batch` matrices of rows x cols, through a 32 x 33 LDS tile
+// so both the reads and the writes of a wavefront are consecutive. Grid: x over the 32 x 32
+// tiles of one matrix, y over the matrices.
+__global__ void __launch_bounds__(THREADS)
+transpose_kernel(const float* __restrict__ src, float* __restrict__ dst, int rows, int cols,
+                 int tiles_c) {
+    __shared__ float tile[32][33];
+    const int tr = blockIdx.x / tiles_c, tc = blockIdx.x - tr * tiles_c;
+    const size_t off = (size_t)blockIdx.y * rows * cols;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = tr * 32 + ty + 8 * i, c = tc * 32 + tx;
+        if (r < rows && c < cols) tile[ty + 8 * i][tx] = src[off + (size_t)r * cols + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tc * 32 + ty + 8 * i, r = tr * 32 + tx;
+        if (r < rows && c < cols) dst[off + (size_t)c * rows + r] = tile[tx][ty + 8 * i];
+    }
+}
+
 // rows[w][f] = t[n][f][p] for w = n * P + p (dY to one row per window).
 __global__ void __launch_bounds__(THREADS)
 nfp_to_rows_kernel(const float* __restrict__ t, float* __restrict__ rows, Geom g) {
@@ -666,6 +689,25 @@ void launch_im2col(const float* x, float* cols, const Geom& g, hipStream_t strea
     }
 }
 
+// [N][F][P] -> [N * P][F] (to_rows) or back, as N transposes of F x P matrices; the element-
+// wise kernels when N exceeds the grid's y range.
+void launch_nfp_rows(const float* src, float* dst, const Geom& g, bool to_rows, hipStream_t stream) {
+    const int rows = to_rows ? g.F : g.P, cols = to_rows ? g.P : g.F;
+    if (g.N <= 65535) {
+        const int tiles_r = (rows + 31) / 32, tiles_c = (cols + 31) / 32;
+        hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)(tiles_r * tiles_c), (unsigned)g.N),
+                           dim3(THREADS), 0, stream, src, dst, rows, cols, tiles_c);
+        return;
+    }
+    const size_t outn = (size_t)g.windows * g.F;
+    if (to_rows)
+        hipLaunchKernelGGL(nfp_to_rows_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
+                           stream, src, dst, g);
+    else
+        hipLaunchKernelGGL(rows_to_nfp_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
+                           stream, src, dst, g);
+}
+
 int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_conv_shape* s, int S,
              int algo, void* workspace, size_t workspace_bytes, void* stream_) {
     if (!a || !b || !out) return hipErrorInvalidValue;
@@ -701,7 +743,6 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
     }
     char* base = static_cast<char*>(workspace);
     char* gws = base + p.gemm;
-    const size_t outn = (size_t)g.windows * g.F;
     switch (kind) {
         case Kind::Forward: {
             float* yrows = reinterpret_cast<float*>(base + p.buf1);
@@ -722,15 +763,13 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
                                 dense_addressing(p.L));
             }
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL(rows_to_nfp_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
-                               stream, yrows, out, g);
+            launch_nfp_rows(yrows, out, g, false, stream);
             break;
         }
         case Kind::GradWeight: {
             float* dyrows = reinterpret_cast<float*>(base + p.buf0);
             float* cols = reinterpret_cast<float*>(base + p.buf1);
-            hipLaunchKernelGGL(nfp_to_rows_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
-                               stream, a, dyrows, g);
+            launch_nfp_rows(a, dyrows, g, true, stream);
             launch_im2col(b, cols, g, stream);
             e = gemm_launch(dyrows, cols, out, p.L, gws, stream, nullptr, GemmOptions(),
                             dense_addressing(p.L));
@@ -739,8 +778,7 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
         }
         case Kind::GradInput: {
             float* dyrows = reinterpret_cast<float*>(base + p.buf0);
-            hipLaunchKernelGGL(nfp_to_rows_kernel, dim3((unsigned)grid_for(outn)), dim3(THREADS), 0,
-                               stream, a, dyrows, g);
+            launch_nfp_rows(a, dyrows, g, true, stream);
             GemmOptions opt;
             opt.group_a = g.K;   // rows of op(A) are the positions: one scale for all weights
             opt.group_b = g.P;   // rows of op(B)^T are the windows: one scale per image
