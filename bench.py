@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 # HBM bytes per launch of the contraction at 4096^3 S=3 (fetch + write), from rocprofv3
 # FETCH_SIZE / WRITE_SIZE scaled by the same counters on a 256 MiB device copy; see
 # profiles/contract_mfma_4096cube_traffic.md. Updated when the kernel changes.
-TRAFFIC_BYTES = 671529280
+TRAFFIC_BYTES = 671543144
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
@@ -441,6 +441,32 @@ def widened(torch, rg, cpu=True, threads=16):
                                              ("dW", dy.cpu().numpy(), x.cpu().numpy()),
                                              ("dX", dy.cpu().numpy(), w.cpu().numpy())], outs))
     line["conv"] = convs
+    # A ResNet-sized layer (batch 32, 64 -> 64 channels, 56 x 56, 3 x 3, padding 1): all three
+    # passes take the GEMM pipeline (forward on the implicit im2col matrix). GPU time and the
+    # same bits on a repeat; no CPU check at this size.
+    g = rg.ConvShape(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1)
+    x = torch.randn(g.N, g.C, g.H, g.W, device="cuda")
+    w = 0.1 * torch.randn(g.F, g.C, g.KH, g.KW, device="cuda")
+    dy = 1e-3 * torch.randn(g.N, g.F, g.OH, g.OW, device="cuda")
+    big = {"case": "resnet-like 32x64x56x56, 64 filters 3x3", "shape": list(g.astuple())}
+    for kind, fn, ws_fn, a, b, o in (("fwd", rg.repro_conv2d_ws, rg.conv2d_workspace, x, w, torch.empty_like(dy)),
+                                      ("dW", rg.repro_conv2d_grad_weight_ws, rg.conv2d_grad_weight_workspace, dy, x, torch.empty_like(w)),
+                                      ("dX", rg.repro_conv2d_grad_input_ws, rg.conv2d_grad_input_workspace, dy, w, torch.empty_like(x))):
+        ws = torch.empty(max(ws_fn(g, 3), 1), dtype=torch.uint8, device="cuda")
+
+        def run():
+            code = fn(a.data_ptr(), b.data_ptr(), o.data_ptr(), g, 3, ws.data_ptr(), ws.numel(), stream())
+            if code != 0:
+                raise rg.ReproGemmError(code, "conv " + kind)
+
+        big[kind + "_gpu_ms"] = round(_gpu_ms(torch, run, reps=10), 4)
+        first = o.clone()
+        run()
+        torch.cuda.synchronize()
+        big[kind + "_same_bits"] = bool(torch.equal(first.view(torch.int32), o.view(torch.int32)))
+        big[kind + "_algo"] = "gemm"
+        del ws
+    line["conv_large"] = big
     # Attention heads as one strided-batched GEMM vs one GEMM per head (GPT-2 small: 12 heads,
     # 1024 tokens, head size 64): scores = Q_h K_h^T and out = P_h V_h, read in place.
     T, H, D = 1024, 12, 64
