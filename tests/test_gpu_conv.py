@@ -154,6 +154,25 @@ def test_direct_and_gemm_algorithms_match_oracle(torch_gpu, S):
             RC.conv2d_algo_workspace(RC.GRAD_WEIGHT, g, S, RC.ALGO_DIRECT)
 
 
+def test_gemm_pipeline_beyond_65535_images(torch_gpu):
+    """More images than a grid's y dimension holds: the [N][F][P] <-> [N*P][F] reorders fall
+    back from the tiled transposes to their element-wise kernels (GEMM algorithm forced)."""
+    torch = torch_gpu
+    shape = (65537, 2, 3, 2, 3, 2, 1, 1, 1, 0, 0)
+    N, C, H, W, F, KH, KW = shape[:7]
+    OH, OW = O.conv_out_hw(shape)
+    rng = np.random.default_rng(65537)
+    x = rng.standard_normal(N * C * H * W).astype(np.float32)
+    w = (rng.standard_normal(F * C * KH * KW) * 0.1).astype(np.float32)
+    dy = (rng.standard_normal((N, F * OH * OW)) *
+          (np.float32(2.0) ** rng.integers(-20, 20, (N, 1)))).astype(np.float32).reshape(-1)
+    for kind, a, b in (("fwd", x, w), ("dW", dy, x), ("dX", dy, w)):
+        note("conv 65537 images", kind)
+        got = _run_algo(torch, kind, a, b, shape, 3, RC.ALGO_GEMM)
+        want = _oracle(kind, a, b, shape, 3)
+        assert np.array_equal(got.view(np.uint32).reshape(-1), want.view(np.uint32).reshape(-1)), kind
+
+
 def test_direct_sums_at_their_exactness_limit(torch_gpu):
     """Every value 127 = 127 * 2^0, which its scale (2^0) maps to the largest fixed-point
     value X = 127 * 2^14: the central pixel's input-gradient sum has 2048 products of
