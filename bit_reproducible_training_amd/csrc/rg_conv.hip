@@ -73,24 +73,67 @@ Geom geom(const rg_conv_shape& s) {
 size_t grid_for(size_t n) { return std::min<size_t>((n + THREADS - 1) / THREADS, 65536); }
 
 // cols[w][k] = x at position k = (c, ky, kx) of window w = (n, oy, ox), zero in the padding,
-// for the `count` elements from window w0 on.
+// for the windows w0 .. w0 + count - 1. A block moves a tile of 64 windows x 64 positions
+// through LDS: it reads along the windows (consecutive windows of an output row are consecutive
+// pixels of x, so the loads coalesce) and writes along the positions (256 contiguous bytes of a
+// row of cols per wave).
+constexpr int IM2COL_TILE = 64;
+
 __global__ void __launch_bounds__(THREADS)
 im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uint32_t w0,
               uint32_t count) {
-    for (uint32_t i = blockIdx.x * THREADS + threadIdx.x; i < count; i += gridDim.x * THREADS) {
-        const uint32_t wl = fdiv(i, g.dK);
-        const int k = (int)(i - wl * (uint32_t)g.K);
-        const uint32_t w = w0 + wl;
+    __shared__ float tile[IM2COL_TILE][IM2COL_TILE + 1];
+    __shared__ long long koff[IM2COL_TILE];           // (c*H + ky)*W + kx of each position
+    __shared__ int kys[IM2COL_TILE], kxs[IM2COL_TILE];
+    const int t = threadIdx.x;
+    const uint32_t wt = blockIdx.y * IM2COL_TILE;     // first window of the tile, from w0
+    const int kt = blockIdx.x * IM2COL_TILE;          // first position of the tile
+    if (t < IM2COL_TILE) {
+        const int k = min(kt + t, g.K - 1);
+        const int c = (int)fdiv(k, g.dKHW), r = k - c * (g.KH * g.KW);
+        const int ky = (int)fdiv(r, g.dKW), kx = r - ky * g.KW;
+        koff[t] = ((long long)c * g.H + ky) * g.W + kx;
+        kys[t] = ky;
+        kxs[t] = kx;
+    }
+    __syncthreads();
+    {
+        const int wl = t % IM2COL_TILE;
+        const uint32_t w = w0 + wt + wl;
+        const bool live = wt + wl < count;
         const uint32_t n = fdiv(w, g.dP);
         const int p = (int)(w - n * (uint32_t)g.P);
         const int oy = (int)fdiv(p, g.dOW), ox = p - oy * g.OW;
-        const int c = (int)fdiv(k, g.dKHW), r = k - c * (g.KH * g.KW);
-        const int ky = (int)fdiv(r, g.dKW), kx = r - ky * g.KW;
-        const int y = oy * g.SY - g.PY + ky, xx = ox * g.SX - g.PX + kx;
-        float v = 0.0f;
-        if (y >= 0 && y < g.H && xx >= 0 && xx < g.W)
-            v = x[((n * (uint32_t)g.C + c) * g.H + y) * (uint32_t)g.W + xx];
-        cols[(size_t)w0 * g.K + i] = v;
+        const int y0 = oy * g.SY - g.PY, x0 = ox * g.SX - g.PX;
+        const long long base = (long long)n * g.C * g.H * g.W + (long long)y0 * g.W + x0;
+#pragma unroll
+        for (int kl = t / IM2COL_TILE; kl < IM2COL_TILE; kl += THREADS / IM2COL_TILE) {
+            const int y = y0 + kys[kl], xx = x0 + kxs[kl];
+            float v = 0.0f;
+            if (live && kl < g.K - kt && (unsigned)y < (unsigned)g.H && (unsigned)xx < (unsigned)g.W)
+                v = x[base + koff[kl]];
+            tile[wl][kl] = v;
+        }
+    }
+    __syncthreads();
+    if (g.K % 4 == 0 && g.K - kt >= IM2COL_TILE && (reinterpret_cast<uintptr_t>(cols) & 15) == 0) {
+        // Rows stay 16-byte aligned: 16 lanes store one row's 64 positions as float4s.
+        const int q = t % (IM2COL_TILE / 4);
+        float* out = cols + ((size_t)w0 + wt) * g.K + kt + 4 * q;
+#pragma unroll
+        for (int wl = t / (IM2COL_TILE / 4); wl < IM2COL_TILE; wl += THREADS / (IM2COL_TILE / 4))
+            if (wt + wl < count)
+                *reinterpret_cast<float4*>(out + (size_t)wl * g.K) =
+                    make_float4(tile[wl][4 * q], tile[wl][4 * q + 1], tile[wl][4 * q + 2],
+                                tile[wl][4 * q + 3]);
+    } else {
+        const int kl = t % IM2COL_TILE;
+        if (kl < g.K - kt) {
+            float* out = cols + ((size_t)w0 + wt) * g.K + kt + kl;
+#pragma unroll
+            for (int wl = t / IM2COL_TILE; wl < IM2COL_TILE; wl += THREADS / IM2COL_TILE)
+                if (wt + wl < count) out[(size_t)wl * g.K] = tile[wl][kl];
+        }
     }
 }
 
@@ -678,14 +721,17 @@ int conv_plan(Kind kind, const rg_conv_shape* s, int S, int algo, ConvPlan* P) {
     return hipSuccess;
 }
 
-// cols for every window, in launches of fewer than 2^31 elements.
+// cols for every window. Consecutive blocks take the position tiles of one window tile (grid
+// x), so a row of cols is completed, and its patch of x read, by neighbouring blocks; launches
+// of at most 65535 window tiles (grid y).
 void launch_im2col(const float* x, float* cols, const Geom& g, hipStream_t stream) {
-    const long long per = std::max<long long>(1, (long long)INT_MAX / g.K);
+    const long long per = 65535LL * IM2COL_TILE;
+    const unsigned ktiles = (unsigned)((g.K + IM2COL_TILE - 1) / IM2COL_TILE);
     for (long long w0 = 0; w0 < g.windows; w0 += per) {
         const long long nw = std::min<long long>(per, g.windows - w0);
-        const uint32_t count = (uint32_t)(nw * g.K);
-        hipLaunchKernelGGL(im2col_kernel, dim3((unsigned)grid_for(count)), dim3(THREADS), 0, stream,
-                           x, cols, g, (uint32_t)w0, count);
+        const unsigned wtiles = (unsigned)((nw + IM2COL_TILE - 1) / IM2COL_TILE);
+        hipLaunchKernelGGL(im2col_kernel, dim3(ktiles, wtiles), dim3(THREADS), 0, stream, x, cols,
+                           g, (uint32_t)w0, (uint32_t)nw);
     }
 }
 
