@@ -42,7 +42,7 @@ struct Geom {
     int OH, OW, P;      // output size, P = OH * OW windows per image
     int K;              // C * KH * KW positions per window
     long long windows;  // N * P
-    FastDiv dK, dP, dOW, dKHW, dKW, dF, dFP, dW, dH, dC, dSY, dSX;
+    FastDiv dK, dP, dOW, dKHW, dKW, dF, dFP, dW, dH, dC, dN, dSY, dSX;
 };
 
 Geom geom(const rg_conv_shape& s) {
@@ -64,6 +64,7 @@ Geom geom(const rg_conv_shape& s) {
     g.dFP = make_fastdiv((uint32_t)((long long)g.F * g.P));
     g.dW = make_fastdiv(g.W);
     g.dH = make_fastdiv(g.H);
+    g.dN = make_fastdiv(g.N);
     g.dC = make_fastdiv(g.C);
     g.dSY = make_fastdiv(g.SY);
     g.dSX = make_fastdiv(g.SX);
@@ -196,10 +197,16 @@ __device__ __forceinline__ int window_at(int v, int pad, int k, const FastDiv& d
 // dX[n][c][y][x]: the exact int64 sum of T[w][k] (summed over the split parts) over every
 // window w that reads pixel (y, x) at position k = (c, ky, kx), rounded once. T is stored
 // transposed, [k][w]: for one (ky, kx) the threads of a pixel row read consecutive windows.
+// Pixels are taken channel by channel across the images, (c, n, y, x), so that the KH*KW rows
+// of T^T of a channel are read from start to end.
 // ea: the positions' exponents (all the weights' one), eb: the windows' (their image's).
+// KHT x KWT: the filter size when known at compile time (0: g.KH x g.KW), so that the loads
+// of every (ky, kx) are predicated and in flight together.
+template <int KHT, int KWT>
 __global__ void __launch_bounds__(THREADS)
 col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __restrict__ ea,
                     const int* __restrict__ eb, float* __restrict__ dx, Geom g, int e0) {
+    const int KH = KHT ? KHT : g.KH, KW = KWT ? KWT : g.KW;
     const uint32_t total = (uint32_t)((long long)g.N * g.C * g.H * g.W);
     const size_t MN = (size_t)g.windows * g.K;
     const int eW = ea[0];
@@ -208,21 +215,28 @@ col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __re
         const int xx = (int)(i - q1 * (uint32_t)g.W);
         const uint32_t q2 = fdiv(q1, g.dH);
         const int y = (int)(q1 - q2 * (uint32_t)g.H);
-        const uint32_t n = fdiv(q2, g.dC);
-        const int c = (int)(q2 - n * (uint32_t)g.C);
+        const uint32_t c = fdiv(q2, g.dN);
+        const uint32_t n = q2 - c * (uint32_t)g.N;
+        const int64_t* pc = part + (size_t)c * KH * KW * g.windows + (size_t)n * g.P;
+        const int e = eb[(size_t)n * g.P] + eW + e0;
         int64_t t = 0;
-        for (int ky = 0; ky < g.KH; ++ky) {
-            const int oy = window_at(y, g.PY, ky, g.dSY, g.SY, g.OH);
-            if (oy < 0) continue;
-            for (int kx = 0; kx < g.KW; ++kx) {
-                const int ox = window_at(xx, g.PX, kx, g.dSX, g.SX, g.OW);
-                if (ox < 0) continue;
-                const size_t w = (size_t)n * g.P + (size_t)oy * g.OW + ox;
-                const size_t at = (((size_t)c * g.KH + ky) * g.KW + kx) * g.windows + w;
-                for (int s = 0; s < split; ++s) t += part[(size_t)s * MN + at];
+        for (int s = 0; s < split; ++s, pc += MN) {
+            // Every position loads (a window that does not exist reads the start of its row of
+            // T^T, in bounds, and adds zero), so the KH*KW loads are independent.
+#pragma unroll
+            for (int ky = 0; ky < KH; ++ky) {
+                const int oy = window_at(y, g.PY, ky, g.dSY, g.SY, g.OH);
+#pragma unroll
+                for (int kx = 0; kx < KW; ++kx) {
+                    const int ox = window_at(xx, g.PX, kx, g.dSX, g.SX, g.OW);
+                    const bool ok = oy >= 0 && ox >= 0;
+                    const int64_t v = pc[(size_t)(ky * KW + kx) * g.windows + (ok ? oy * g.OW + ox : 0)];
+                    t += ok ? v : 0;
+                }
             }
         }
-        dx[i] = repro_gemm::round_to_float_fast(t, eb[(size_t)n * g.P] + eW + e0);
+        dx[((size_t)n * g.C + c) * g.H * g.W + (size_t)y * g.W + xx] =
+            repro_gemm::round_to_float_fast(t, e);
     }
 }
 
@@ -833,8 +847,11 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
                             dense_addressing(p.L));
             if (e != hipSuccess) return e;
             const size_t pixels = (size_t)g.N * g.C * g.H * g.W;
-            hipLaunchKernelGGL(col2im_round_kernel, dim3((unsigned)grid_for(pixels)), dim3(THREADS),
-                               0, stream, reinterpret_cast<const int64_t*>(gws + p.L.part),
+            const auto col2im = g.KH == 3 && g.KW == 3   ? col2im_round_kernel<3, 3>
+                                : g.KH == 5 && g.KW == 5 ? col2im_round_kernel<5, 5>
+                                : g.KH == 1 && g.KW == 1 ? col2im_round_kernel<1, 1>
+                                                         : col2im_round_kernel<0, 0>;
+            hipLaunchKernelGGL(col2im, dim3((unsigned)grid_for(pixels)), dim3(THREADS), 0, stream, reinterpret_cast<const int64_t*>(gws + p.L.part),
                                p.L.split, reinterpret_cast<const int*>(gws + p.L.ea),
                                reinterpret_cast<const int*>(gws + p.L.eb), out, g, -14 * (S - 1));
             break;
