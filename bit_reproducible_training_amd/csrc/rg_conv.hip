@@ -107,8 +107,10 @@ im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uin
         const int oy = (int)fdiv(p, g.dOW), ox = p - oy * g.OW;
         const int y0 = oy * g.SY - g.PY, x0 = ox * g.SX - g.PX;
         const long long base = (long long)n * g.C * g.H * g.W + (long long)y0 * g.W + x0;
+        constexpr int STEP = THREADS / IM2COL_TILE;
 #pragma unroll
-        for (int kl = t / IM2COL_TILE; kl < IM2COL_TILE; kl += THREADS / IM2COL_TILE) {
+        for (int j = 0; j < IM2COL_TILE / STEP; ++j) {
+            const int kl = t / IM2COL_TILE + j * STEP;
             const int y = y0 + kys[kl], xx = x0 + kxs[kl];
             float v = 0.0f;
             if (live && kl < g.K - kt && (unsigned)y < (unsigned)g.H && (unsigned)xx < (unsigned)g.W)
@@ -121,19 +123,25 @@ im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uin
         // Rows stay 16-byte aligned: 16 lanes store one row's 64 positions as float4s.
         const int q = t % (IM2COL_TILE / 4);
         float* out = cols + ((size_t)w0 + wt) * g.K + kt + 4 * q;
+        constexpr int STEP = THREADS / (IM2COL_TILE / 4);
 #pragma unroll
-        for (int wl = t / (IM2COL_TILE / 4); wl < IM2COL_TILE; wl += THREADS / (IM2COL_TILE / 4))
+        for (int j = 0; j < IM2COL_TILE / STEP; ++j) {
+            const int wl = t / (IM2COL_TILE / 4) + j * STEP;
             if (wt + wl < count)
                 *reinterpret_cast<float4*>(out + (size_t)wl * g.K) =
                     make_float4(tile[wl][4 * q], tile[wl][4 * q + 1], tile[wl][4 * q + 2],
                                 tile[wl][4 * q + 3]);
+        }
     } else {
         const int kl = t % IM2COL_TILE;
         if (kl < g.K - kt) {
             float* out = cols + ((size_t)w0 + wt) * g.K + kt + kl;
+            constexpr int STEP = THREADS / IM2COL_TILE;
 #pragma unroll
-            for (int wl = t / IM2COL_TILE; wl < IM2COL_TILE; wl += THREADS / IM2COL_TILE)
+            for (int j = 0; j < IM2COL_TILE / STEP; ++j) {
+                const int wl = t / IM2COL_TILE + j * STEP;
                 if (wt + wl < count) out[(size_t)wl * g.K] = tile[wl][kl];
+            }
         }
     }
 }
@@ -207,6 +215,7 @@ __global__ void __launch_bounds__(THREADS)
 col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __restrict__ ea,
                     const int* __restrict__ eb, float* __restrict__ dx, Geom g, int e0) {
     const int KH = KHT ? KHT : g.KH, KW = KWT ? KWT : g.KW;
+    constexpr int UNROLL_Y = KHT > 0 ? KHT : 1, UNROLL_X = KWT > 0 ? KWT : 1;
     const uint32_t total = (uint32_t)((long long)g.N * g.C * g.H * g.W);
     const size_t MN = (size_t)g.windows * g.K;
     const int eW = ea[0];
@@ -223,10 +232,10 @@ col2im_round_kernel(const int64_t* __restrict__ part, int split, const int* __re
         for (int s = 0; s < split; ++s, pc += MN) {
             // Every position loads (a window that does not exist reads the start of its row of
             // T^T, in bounds, and adds zero), so the KH*KW loads are independent.
-#pragma unroll
+#pragma unroll UNROLL_Y
             for (int ky = 0; ky < KH; ++ky) {
                 const int oy = window_at(y, g.PY, ky, g.dSY, g.SY, g.OH);
-#pragma unroll
+#pragma unroll UNROLL_X
                 for (int kx = 0; kx < KW; ++kx) {
                     const int ox = window_at(xx, g.PX, kx, g.dSX, g.SX, g.OW);
                     const bool ok = oy >= 0 && ox >= 0;
