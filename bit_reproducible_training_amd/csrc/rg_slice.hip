@@ -31,13 +31,20 @@ __device__ __forceinline__ float max4(float4 v) {
 // Row access, element (r, k) of item b at src[b*bstride + r*ld + k]: wavefront w of the
 // operand handles row w / nch of all items' rows (item-major), chunk w % nch.
 // (row, chunk) pairs per wavefront in the row-access maxima: a lane per pair for short
-// chunks (a wavefront per pair would leave most lanes idle), else the whole wavefront.
-__host__ __device__ inline int rows_per_wave(const SliceDesc& d) { return d.kch <= 32 ? 64 : 1; }
+// chunks (a wavefront per pair would leave most lanes idle); for 16-byte rows with chunks of
+// at most 128 values, 16 or 32 lanes per pair (one float4 each per step); else the whole
+// wavefront.
+__host__ __device__ inline int rows_per_wave(const SliceDesc& d) {
+    if (d.kch <= 32) return 64;
+    if (d.vec && d.kch <= 64) return 4;
+    if (d.vec && d.kch <= 128) return 2;
+    return 1;
+}
 
 template <int WAVES>
 __device__ void absmax_rows(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63;
-    if (rows_per_wave(d) > 1) {
+    if (rows_per_wave(d) == 64) {
         const long long pair = (blk * WAVES + (threadIdx.x >> 6)) * 64 + lane;
         if (pair >= (long long)d.batch * d.R * d.nch) return;
         const long long i = pair / d.nch;
@@ -48,6 +55,27 @@ __device__ void absmax_rows(const SliceDesc& d, long long blk) {
         float m = 0.0f;
         for (int k = k0; k < k1; ++k) m = fmaxf(m, fabsf(row[k]));
         d.pmax[(size_t)c * d.batch * d.Rp + (size_t)b * d.Rp + r] = m;
+        return;
+    }
+    if (rows_per_wave(d) > 1) {  // vec: lpr lanes per pair, float4 loads, shuffle reduction
+        const int rpw = rows_per_wave(d), lpr = 64 / rpw;
+        const long long pair = (blk * WAVES + (threadIdx.x >> 6)) * rpw + lane / lpr;
+        const bool live = pair < (long long)d.batch * d.R * d.nch;
+        float m = 0.0f;
+        long long i = 0;
+        int c = 0, b = 0, r = 0;
+        if (live) {
+            i = pair / d.nch;
+            c = (int)(pair - i * d.nch);
+            b = (int)(i / d.R);
+            r = (int)(i - (long long)b * d.R);
+            const float4* p =
+                reinterpret_cast<const float4*>(d.src + (size_t)b * d.bstride + (size_t)r * d.ld);
+            const int q1 = min(d.K, c * d.kch + d.kch) / 4;
+            for (int q = c * d.kch / 4 + lane % lpr; q < q1; q += lpr) m = fmaxf(m, max4(p[q]));
+        }
+        for (int o = 1; o < lpr; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (live && lane % lpr == 0) d.pmax[(size_t)c * d.batch * d.Rp + (size_t)b * d.Rp + r] = m;
         return;
     }
     const long long w = blk * WAVES + (threadIdx.x >> 6);
