@@ -350,8 +350,7 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
         else launch_split(two, none, L.S, i32, stream);
     } else {
         launch_absmax(da, db, stream);
-        if (opt.group_a > 0) launch_group_max(da, opt.group_a, stream);
-        if (opt.group_b > 0) launch_group_max(db, opt.group_b, stream);
+        launch_group_max2(&da, opt.group_a, &db, opt.group_b, stream);
         launch_split(da, db, L.S, i32, stream);
     }
     record(1);

@@ -188,6 +188,9 @@ void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream);
 void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream);
 // Replaces the partial row maxima of d by the maximum over each group of `group` rows.
 void launch_group_max(const SliceDesc& d, int group, hipStream_t stream);
+// Both operands' group maxima in one launch (a null operand or a group <= 0 is skipped).
+void launch_group_max2(const SliceDesc* a, int group_a, const SliceDesc* b, int group_b,
+                       hipStream_t stream);
 // Output addressing of the contraction and the final rounding: C of item b at
 // C + b * c_item, rows ldc apart.
 struct OutAddr {

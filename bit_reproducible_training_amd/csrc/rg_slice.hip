@@ -759,30 +759,54 @@ void slice_grid(SliceDesc& d) {
 // Group scales: every row of each group of `group` consecutive rows gets the group's largest
 // magnitude. Block g reduces the partial maxima pmax[c][r] of its rows over every chunk c,
 // then writes the maximum back to all of them, so the split sees one maximum per group.
-__global__ void __launch_bounds__(256)
-group_max_kernel(float* __restrict__ pmax, int R, int Rp, int nch, int group) {
+// GroupMax: one operand's share of a launch, its blocks [0, blocks).
+struct GroupMax {
+    float* pmax;
+    int R, Rp, nch, group, blocks;
+};
+
+__device__ void group_max_block(const GroupMax& d, int blk) {
     __shared__ float red[4];
-    const int r0 = blockIdx.x * group;
-    const int rows = min(R, r0 + group) - r0;
-    const long long n = (long long)rows * nch;
+    const int r0 = blk * d.group;
+    const int r1 = min(d.R, r0 + d.group);
     float m = 0.0f;
-    for (long long i = threadIdx.x; i < n; i += 256) {
-        const int c = (int)(i / rows), r = r0 + (int)(i - (long long)c * rows);
-        m = fmaxf(m, pmax[(size_t)c * Rp + r]);
-    }
+    for (int c = 0; c < d.nch; ++c)
+        for (int r = r0 + (int)threadIdx.x; r < r1; r += 256) m = fmaxf(m, d.pmax[(size_t)c * d.Rp + r]);
     m = wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (long long i = threadIdx.x; i < n; i += 256) {
-        const int c = (int)(i / rows), r = r0 + (int)(i - (long long)c * rows);
-        pmax[(size_t)c * Rp + r] = m;
-    }
+    for (int c = 0; c < d.nch; ++c)
+        for (int r = r0 + (int)threadIdx.x; r < r1; r += 256) d.pmax[(size_t)c * d.Rp + r] = m;
+}
+
+// Both operands' groups in one launch (b.blocks may be 0).
+__global__ void __launch_bounds__(256) group_max_kernel(GroupMax a, GroupMax b) {
+    if ((int)blockIdx.x < a.blocks) group_max_block(a, blockIdx.x);
+    else group_max_block(b, blockIdx.x - a.blocks);
+}
+
+static GroupMax group_max_of(const SliceDesc* d, int group) {
+    GroupMax g{nullptr, 0, 0, 0, 1, 0};
+    if (!d || group <= 0) return g;
+    g.pmax = d->pmax;
+    g.R = d->R;
+    g.Rp = d->Rp;
+    g.nch = d->nch;
+    g.group = group >= d->R ? d->R : group;
+    g.blocks = (d->R + g.group - 1) / g.group;
+    return g;
+}
+
+void launch_group_max2(const SliceDesc* a, int group_a, const SliceDesc* b, int group_b,
+                       hipStream_t stream) {
+    const GroupMax ga = group_max_of(a, group_a), gb = group_max_of(b, group_b);
+    if (ga.blocks + gb.blocks == 0) return;
+    group_max_kernel<<<(unsigned)(ga.blocks + gb.blocks), 256, 0, stream>>>(ga, gb);
 }
 
 void launch_group_max(const SliceDesc& d, int group, hipStream_t stream) {
-    const int g = group >= d.R ? d.R : group;
-    group_max_kernel<<<(unsigned)((d.R + g - 1) / g), 256, 0, stream>>>(d.pmax, d.R, d.Rp, d.nch, g);
+    launch_group_max2(&d, group, nullptr, 0, stream);
 }
 
 void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream) {
