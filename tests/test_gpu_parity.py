@@ -216,6 +216,34 @@ def test_narrow_operands_long_k(torch_gpu, M, N, K, ta, tb):
         assert np.array_equal(bits(C), want), (split, plan.split_k)
 
 
+# Row-access operands of 33-132 values a row through the two-pass slicing (the reference
+# algorithm's int32 digits always take it): the maxima pass gives a 16-byte row 16 or 32 lanes
+# (several rows per wavefront), and a row of K % 4 != 0 values a whole wavefront. Row scales
+# spread over 2^-20 .. 2^20 so every row's own maximum matters.
+SHORT_ROWS = [36, 64, 66, 68, 100, 128, 132]
+
+
+@pytest.mark.parametrize("K", SHORT_ROWS)
+def test_row_maxima_short_rows(torch_gpu, K):
+    torch = torch_gpu
+    M, N = 300, 77
+    rng = np.random.default_rng(K)
+    A = (rng.standard_normal((M, K)) * 2.0 ** rng.integers(-20, 20, (M, 1))).astype(np.float32).ravel()
+    B = (rng.standard_normal((N, K)) * 2.0 ** rng.integers(-20, 20, (N, 1))).astype(np.float32).ravel()
+    X, Y, eA, eB = O.quantize(A, B, M, N, K, 0, 1, 3)
+    want = O.cpu_gemm(A, B, M, N, K, 0, 1, 3).view(np.uint32)
+    dA, dB = to_dev(torch, A), to_dev(torch, B)
+    for algo in (rg.Algo.Reference, rg.Algo.TensorCore):
+        cfg = rg.Config(algo=algo, trans_b=True)
+        note("short rows K=%d algo=%s" % (K, algo.name))
+        C, plan, ws = run(torch, dA, dB, M, N, K, cfg)
+        info = rg.workspace_layout(M, N, K, cfg)
+        w = ws.cpu().numpy()
+        for R, eo, eoff in ((info.Mp, eA, info.ea), (info.Np, eB, info.eb)):
+            assert np.array_equal(w[eoff:eoff + 4 * R].view(np.int32)[:eo.shape[0]], eo), algo
+        assert np.array_equal(bits(C), want), algo
+
+
 @pytest.mark.parametrize("split", [2, 3])
 def test_contraction_exact_products(torch_gpu, split):
     """Stage check of the contraction: the int64 split-K partials sum to the exact
