@@ -1,9 +1,13 @@
-"""Builds librepro_gemm.so (HIP, gfx950) in-tree with hipcc.
+"""Builds librepro_gemm.so (HIP, gfx950) and its PyTorch binding in-tree.
 
-The library is compiled from the sources under csrc/ into
+The library is compiled with hipcc from the sources under csrc/ into
 bit_reproducible_training_amd/librepro_gemm.so, next to this file, so it travels with
 the repository. Flags that affect results: no fast-math, no denormal flushing,
 correctly rounded fp32 division (hipcc's default), no FP contraction.
+
+The binding (csrc/rg_torch.cpp -> _backend<python suffix>.so) is host C++ compiled with g++
+against PyTorch's headers; it calls the library through its C ABI and carries the CPU
+implementation (include/repro_*_cpu.h) for CPU tensors.
 """
 import os
 import subprocess
@@ -18,6 +22,7 @@ BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "librepro_gemm.so")
 
 SOURCES = ["rg_slice.hip", "rg_contract.hip", "rg_probe.hip", "rg_sum.hip", "rg_conv.hip", "rg_api.cpp"]
+BINDING_SOURCE = "rg_torch.cpp"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -47,8 +52,40 @@ def _run(cmd):
     return out
 
 
+def binding_path():
+    import sysconfig
+
+    return os.path.join(PKG_DIR, "_backend" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _binding_compile_cmd(obj):
+    import sysconfig
+
+    import torch
+
+    tdir = os.path.dirname(torch.__file__)
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-fno-fast-math", "-ffp-contract=off", "-pthread",
+            "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", "-DTORCH_EXTENSION_NAME=_backend",
+            "-DTORCH_API_INCLUDE_EXTENSION_H",
+            "-D_GLIBCXX_USE_CXX11_ABI=%d" % int(torch._C._GLIBCXX_USE_CXX11_ABI),
+            "-I", INCLUDE, "-I", os.path.join(tdir, "include"),
+            "-I", os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+            "-I", "/opt/rocm/include", "-I", sysconfig.get_paths()["include"],
+            "-c", os.path.join(CSRC, BINDING_SOURCE), "-o", obj]
+
+
+def _binding_link_cmd(obj, out):
+    import torch
+
+    tlib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    return ["g++", "-shared", "-pthread", obj, "-o", out, "-L", PKG_DIR, "-l:librepro_gemm.so",
+            "-L", tlib, "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+            "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + tlib]
+
+
 def build(verbose=False):
-    """Compiles every source and links the shared library. Always recompiles."""
+    """Compiles every source, links the shared library and the PyTorch binding. Always
+    recompiles."""
     os.makedirs(BUILD_DIR, exist_ok=True)
 
     def compile_one(src):
@@ -61,11 +98,17 @@ def build(verbose=False):
             print(out, file=sys.stderr)
         return obj
 
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    binding_obj = os.path.join(BUILD_DIR, "rg_torch.o")
+    with ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as ex:
+        binding = ex.submit(_run, _binding_compile_cmd(binding_obj))
         objs = list(ex.map(compile_one, SOURCES))
+        binding.result()
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs)
     os.replace(tmp, LIB_PATH)
+    out = binding_path()
+    _run(_binding_link_cmd(binding_obj, out + ".tmp"))
+    os.replace(out + ".tmp", out)
     return LIB_PATH
 
 

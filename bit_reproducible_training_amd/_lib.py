@@ -1,9 +1,10 @@
-"""ctypes bindings of librepro_gemm.so (the C ABI in include/repro_gemm.h,
-include/repro_sum.h and include/repro_conv.h).
+"""Loads librepro_gemm.so (the C ABI in include/repro_gemm.h, include/repro_sum.h and
+include/repro_conv.h) through ctypes, and the compiled PyTorch binding (_backend) that calls the
+same library for tensors.
 
-The library must have been built (bit_reproducible_training_amd._build.build(), or
-__graft_entry__.build()). There is no fallback: if the library is missing or does
-not load, importing this module raises.
+Both must have been built (bit_reproducible_training_amd._build.build(), or
+__graft_entry__.build()). There is no fallback: if either is missing or does not load,
+importing this module raises.
 """
 import ctypes
 import os
@@ -150,14 +151,9 @@ def _bind_after_torch():
     dynamic loader would bind the system runtime, and a later `import torch` would map a
     second HIP runtime into the process, which breaks both. Importing torch first lets the
     loader resolve this library's libamdhip64.so.7 to torch's already-loaded copy.
-    Set RG_NO_TORCH=1 in processes that never use torch to skip the import.
+    The compiled binding links libtorch as well.
     """
-    if os.environ.get("RG_NO_TORCH") == "1":
-        return
-    try:
-        import torch  # noqa: F401
-    except ImportError:
-        pass
+    import torch  # noqa: F401
 
 
 def hip_runtimes_mapped():
@@ -186,6 +182,21 @@ def _load():
 
 
 lib = _load()
+
+
+def _load_backend():
+    """The compiled binding, after torch (it links libtorch) and after librepro_gemm.so, which
+    it uses through the same mapping."""
+    import importlib
+
+    try:
+        return importlib.import_module(__package__ + "._backend")
+    except ImportError as e:
+        raise ImportError("the PyTorch binding _backend is not built (%s); run "
+                          "__graft_entry__.build()" % e) from e
+
+
+_backend = _load_backend()
 
 
 def error_string(code):

@@ -4,15 +4,16 @@ Names and argument meaning follow repro_conv_cuda/repro_conv.cuh:19-31 (ConvShap
 conv2d_workspace, conv2d_grad_weight_workspace, conv2d_grad_input_workspace, repro_conv2d_ws,
 repro_conv2d_grad_weight_ws, repro_conv2d_grad_input_ws) and the PyTorch bindings
 repro_torch/src/bindings.cpp:97-175 (conv2d, conv2d_grad_weight, conv2d_grad_input).
-Everything runs through the C ABI of librepro_gemm.so (include/repro_conv.h) on the GPU;
-there is no CPU path.
+GPU work runs through the C ABI of librepro_gemm.so (include/repro_conv.h); the tensor
+operations go through the compiled binding _backend, which runs CPU tensors on the CPU
+implementation (include/repro_conv_cpu.h) with the same bits.
 """
 import ctypes
 from dataclasses import dataclass
 
 from . import _lib
-from ._lib import lib
-from .repro_gemm import _check, _workspace
+from ._lib import _backend, lib
+from .repro_gemm import _check
 
 
 @dataclass
@@ -116,67 +117,22 @@ def repro_conv2d_algo_ws(pass_, a, b, out, g, S, algo, workspace, workspace_byte
                                  workspace, int(workspace_bytes), stream)
 
 
-def _require(t, name):
-    import torch
-
-    if t.dtype != torch.float32:
-        raise ValueError("%s must be float32" % name)
-    if not t.is_cuda:
-        raise ValueError("%s must be a GPU tensor (no CPU path in this library)" % name)
-    return t.contiguous()
-
-
-def _launch(torch, fn, ws_fn, a, b, out, g, S, what):
-    nbytes = ws_fn(g, S)
-    ws = _workspace(torch, nbytes, a.device)
-    stream = torch.cuda.current_stream(a.device).cuda_stream
-    _check(fn(a.data_ptr(), b.data_ptr(), out.data_ptr(), g, S, ws.data_ptr(), ws.numel(), stream),
-           what)
-    return out
-
-
 def conv2d(x, w, SY, SX, PY, PX, S=3):
-    """out[N][F][OH][OW] from x[N][C][H][W] and w[F][C][KH][KW] (bindings.cpp:112-131)."""
-    import torch
-
-    x = _require(x, "x")
-    w = _require(w, "weight")
-    g = ConvShape(x.shape[0], x.shape[1], x.shape[2], x.shape[3], w.shape[0], w.shape[2],
-                  w.shape[3], SY, SX, PY, PX)
-    if w.shape[1] != g.C:
-        raise ValueError("conv2d: weight channels do not match the input")
-    out = torch.empty((g.N, g.F, g.OH, g.OW), dtype=torch.float32, device=x.device)
-    return _launch(torch, repro_conv2d_ws, conv2d_workspace, x, w, out, g, S, "conv")
+    """out[N][F][OH][OW] from x[N][C][H][W] and w[F][C][KH][KW] (bindings.cpp:112-131), on the
+    tensors' GPU (current stream) or on the CPU (same bits)."""
+    return _backend.conv2d(x, w, int(SY), int(SX), int(PY), int(PX), int(S))
 
 
 def conv2d_grad_weight(dy, x, KH, KW, SY, SX, PY, PX, S=3):
     """dW[F][C][KH][KW] from dY[N][F][OH][OW] and x (bindings.cpp:133-152)."""
-    import torch
-
-    dy = _require(dy, "dy")
-    x = _require(x, "x")
-    g = ConvShape(x.shape[0], x.shape[1], x.shape[2], x.shape[3], dy.shape[1], KH, KW, SY, SX,
-                  PY, PX)
-    if tuple(dy.shape) != (g.N, g.F, g.OH, g.OW):
-        raise ValueError("conv2d_grad_weight: dy shape does not match the convolution")
-    dw = torch.empty((g.F, g.C, KH, KW), dtype=torch.float32, device=x.device)
-    return _launch(torch, repro_conv2d_grad_weight_ws, conv2d_grad_weight_workspace, dy, x, dw,
-                   g, S, "conv weight grad")
+    return _backend.conv2d_grad_weight(dy, x, int(KH), int(KW), int(SY), int(SX), int(PY),
+                                       int(PX), int(S))
 
 
 def conv2d_grad_input(dy, w, x_shape, SY, SX, PY, PX, S=3):
     """dX[N][C][H][W] (x_shape) from dY[N][F][OH][OW] and w (bindings.cpp:154-175)."""
-    import torch
-
-    dy = _require(dy, "dy")
-    w = _require(w, "weight")
-    N, C, H, W = (int(v) for v in x_shape)
-    g = ConvShape(N, C, H, W, w.shape[0], w.shape[2], w.shape[3], SY, SX, PY, PX)
-    if tuple(dy.shape) != (g.N, g.F, g.OH, g.OW) or w.shape[1] != C:
-        raise ValueError("conv2d_grad_input: shapes do not match the convolution")
-    dx = torch.empty((N, C, H, W), dtype=torch.float32, device=dy.device)
-    return _launch(torch, repro_conv2d_grad_input_ws, conv2d_grad_input_workspace, dy, w, dx, g,
-                   S, "conv input grad")
+    return _backend.conv2d_grad_input(dy, w, [int(v) for v in x_shape], int(SY), int(SX),
+                                      int(PY), int(PX), int(S))
 
 
 __all__ = ["ALGO_AUTO", "ALGO_DIRECT", "ALGO_GEMM", "FORWARD", "GRAD_INPUT", "GRAD_WEIGHT",

@@ -4,16 +4,17 @@ Names, fields and error behaviour follow repro_gemm_cuda/repro_gemm.cuh:25-75 (A
 Config, Plan, make_plan, repro_gemm_fp32_ws, repro_gemm_fp32, algo_name) and the
 PyTorch binding repro_torch/src/bindings.cpp:43-66 (gemm). The strided-batched form (bmm,
 repro_gemm_strided_batched_fp32_ws) has no counterpart in the reference, which lists batched
-GEMM for attention as still needed (README.md:29). Everything runs through the
-C ABI of librepro_gemm.so on the GPU; there is no CPU path. Device memory and streams
-come from PyTorch (torch.cuda = HIP on ROCm).
+GEMM for attention as still needed (README.md:29). GPU work runs through the C ABI of
+librepro_gemm.so (ctypes for the raw-pointer entry points, the compiled binding _backend for
+tensors); CPU tensors run the CPU implementation (include/repro_gemm_cpu.h) inside _backend.
+Device memory and streams come from PyTorch (torch.cuda = HIP on ROCm).
 """
 import ctypes
 import enum
 from dataclasses import dataclass
 
 from . import _lib
-from ._lib import lib
+from ._lib import _backend, lib
 
 MAX_SLICES = 3
 
@@ -150,51 +151,36 @@ def algo_name(a):
 
 
 # --------------------------------------------------------------------------------------
-# PyTorch-facing operation (repro_torch/src/bindings.cpp:43-66)
+# PyTorch-facing operations (repro_torch/src/bindings.cpp:43-66): the compiled binding
+# (_backend, csrc/rg_torch.cpp) runs GPU tensors on the library and CPU tensors on the CPU
+# implementation of the same definition.
 # --------------------------------------------------------------------------------------
+_backend.set_error_class(ReproGemmError)
 
-_ws_cache = {}
 
-
-def _workspace(torch, nbytes, device):
-    """A cached uint8 device buffer of at least nbytes per device (grown on demand)."""
-    key = (device.type, device.index)
-    buf = _ws_cache.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
-        _ws_cache[key] = buf
-    return buf
+def workspace(torch, nbytes, device):
+    """A uint8 device buffer of nbytes for one call, from PyTorch's caching allocator on the
+    current stream: the allocator gives it to no other stream's work while this call's kernels
+    may still use it, so calls on different streams (or overlapping a graph replay) never share
+    a workspace."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
 def gemm(A, B, M, N, K, ta=False, tb=False, S=3, cfg=None, out=None):
-    """C[M, N] = op(A) op(B) for float32 GPU tensors, on the current stream.
+    """C[M, N] = op(A) op(B) for float32 tensors, both on one GPU (on the current stream) or
+    both on the CPU (the CPU implementation; the same bits).
 
-    Same argument meaning and checks as the reference binding: A holds M*K values
-    (K x M if ta), B holds N*K values (N x K if tb); both float32. Unlike the
-    reference there is no CPU fallback: CPU tensors raise.
+    Same argument meaning and checks as the reference binding: A holds M*K values (K x M if
+    ta), B holds N*K values (N x K if tb). cfg (a Config) replaces ta, tb and S and adds the
+    planner's options (split_k, block tile, algorithm), which never change a bit. out, if
+    given, must be a contiguous float32 tensor of M*N elements on the inputs' device.
     """
-    import torch
-
-    if A.dtype != torch.float32:
-        raise ValueError("A must be float32")
-    if B.dtype != torch.float32:
-        raise ValueError("B must be float32")
-    if not (A.is_cuda and B.is_cuda):
-        raise ValueError("gemm: A and B must be GPU tensors (no CPU path in this library)")
-    A = A.contiguous()
-    B = B.contiguous()
-    if A.numel() != M * K or B.numel() != N * K:
-        raise ValueError("gemm: shape mismatch")
     if cfg is None:
-        cfg = Config(slices=S, trans_a=bool(ta), trans_b=bool(tb))
-    plan = make_plan(M, N, K, cfg)
-    C = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=A.device)
-    ws = _workspace(torch, plan.workspace_bytes, A.device)
-    stream = torch.cuda.current_stream(A.device).cuda_stream
-    code = repro_gemm_fp32_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, cfg,
-                              ws.data_ptr(), ws.numel(), stream)
-    _check(code, "gemm")
-    return C
+        return _backend.gemm_ex(A, B, int(M), int(N), int(K), bool(ta), bool(tb), int(S), 1, 16, 16,
+                                int(Algo.Auto), out)
+    return _backend.gemm_ex(A, B, int(M), int(N), int(K), bool(cfg.trans_a), bool(cfg.trans_b),
+                            int(cfg.slices), int(cfg.split_k), int(cfg.tile_m), int(cfg.tile_n),
+                            int(cfg.algo), out)
 
 
 def bmm(A, B, ta=False, tb=False, S=3, cfg=None, out=None):
@@ -204,7 +190,9 @@ def bmm(A, B, ta=False, tb=False, S=3, cfg=None, out=None):
     A is [batch, M, K] ([batch, K, M] if ta) and B is [batch, K, N] ([batch, N, K] if tb). They
     may be strided views whose last dimension is contiguous (for example one attention head per
     item of a [T, H * D] activation): the library reads them in place through leading
-    dimensions and batch strides. A batch dimension of size 1 broadcasts. C is [batch, M, N].
+    dimensions and batch strides. A batch dimension of size 1 broadcasts. C is [batch, M, N];
+    out, if given, must be a float32 [batch, M, N] tensor on A's device with a contiguous last
+    dimension. CPU tensors run gemm() item by item.
     """
     import torch
 
@@ -212,12 +200,8 @@ def bmm(A, B, ta=False, tb=False, S=3, cfg=None, out=None):
         raise ValueError("bmm: A and B must be 3-D")
     if A.dtype != torch.float32 or B.dtype != torch.float32:
         raise ValueError("bmm: A and B must be float32")
-    if not (A.is_cuda and B.is_cuda):
-        raise ValueError("bmm: A and B must be GPU tensors (no CPU path in this library)")
-    if A.stride(2) != 1:
-        A = A.contiguous()
-    if B.stride(2) != 1:
-        B = B.contiguous()
+    if A.device != B.device:
+        raise ValueError("bmm: A and B must be on the same device")
     batch = max(A.shape[0], B.shape[0])
     if A.shape[0] not in (1, batch) or B.shape[0] not in (1, batch):
         raise ValueError("bmm: batch sizes differ")
@@ -225,15 +209,29 @@ def bmm(A, B, ta=False, tb=False, S=3, cfg=None, out=None):
     Kb, N = (B.shape[2], B.shape[1]) if tb else (B.shape[1], B.shape[2])
     if Kb != K:
         raise ValueError("bmm: shape mismatch")
-    stride_a = A.stride(0) if A.shape[0] > 1 else 0
-    stride_b = B.stride(0) if B.shape[0] > 1 else 0
     if cfg is None:
         cfg = Config(slices=S, trans_a=bool(ta), trans_b=bool(tb))
+    if out is not None:
+        if out.dtype != torch.float32 or out.device != A.device:
+            raise ValueError("bmm: out must be float32 on the inputs' device")
+        if tuple(out.shape) != (batch, M, N) or out.stride(2) != 1:
+            raise ValueError("bmm: out must be [batch, M, N] with a contiguous last dimension")
+    if not A.is_cuda:
+        C = out if out is not None else torch.empty((batch, M, N), dtype=torch.float32)
+        for b in range(batch):
+            a = A[b if A.shape[0] > 1 else 0]
+            bb = B[b if B.shape[0] > 1 else 0]
+            C[b] = gemm(a, bb, M, N, K, cfg=cfg)
+        return C
+    if A.stride(2) != 1:
+        A = A.contiguous()
+    if B.stride(2) != 1:
+        B = B.contiguous()
+    stride_a = A.stride(0) if A.shape[0] > 1 else 0
+    stride_b = B.stride(0) if B.shape[0] > 1 else 0
     plan = make_plan_strided_batched(M, N, K, batch, cfg)
     C = out if out is not None else torch.empty((batch, M, N), dtype=torch.float32, device=A.device)
-    if C.shape != (batch, M, N) or C.stride(2) != 1:
-        raise ValueError("bmm: out must be [batch, M, N] with a contiguous last dimension")
-    ws = _workspace(torch, plan.workspace_bytes, A.device)
+    ws = workspace(torch, plan.workspace_bytes, A.device)
     stream = torch.cuda.current_stream(A.device).cuda_stream
     code = repro_gemm_strided_batched_fp32_ws(A.data_ptr(), A.stride(1), stride_a, B.data_ptr(),
                                               B.stride(1), stride_b, C.data_ptr(), C.stride(1),

@@ -2,15 +2,17 @@
 
 Names, fields and error behaviour follow repro_sum_cuda/repro_sum.cuh:27-45 (SumConfig,
 SumPlan, make_sum_plan, repro_sum_fp32_ws, repro_sum_fp32) and the PyTorch bindings
-repro_torch/src/bindings.cpp:69-91 (exact_sum) and :286-297 (scan_finite). Everything runs
-through the C ABI of librepro_gemm.so (include/repro_sum.h) on the GPU; there is no CPU path.
+repro_torch/src/bindings.cpp:69-91 (exact_sum) and :286-297 (scan_finite). GPU work runs
+through the C ABI of librepro_gemm.so (include/repro_sum.h); the tensor operations go through the
+compiled binding _backend, which runs CPU tensors on the CPU implementation
+(include/repro_sum_cpu.h) with the same bits.
 """
 import ctypes
 from dataclasses import dataclass
 
 from . import _lib
-from ._lib import lib
-from .repro_gemm import ReproGemmError, _check, _workspace
+from ._lib import _backend, lib
+from .repro_gemm import ReproGemmError, _check
 
 
 @dataclass
@@ -62,44 +64,17 @@ def repro_sum_fp32(x, out, A, B, C, cfg=None, stream=None):
 
 def exact_sum(x, A, B, C, mean=False):
     """out[b] = exact sum over a, c of x[a, b, c] rounded once (divided exactly by A*C when
-    mean), for a float32 GPU tensor x viewed as [A][B][C]; on the current stream.
-
-    Same arguments and checks as the reference binding (bindings.cpp:69-91); CPU tensors
-    raise (no CPU path in this library).
-    """
-    import torch
-
-    if x.dtype != torch.float32:
-        raise ValueError("x must be float32")
-    if not x.is_cuda:
-        raise ValueError("exact_sum: x must be a GPU tensor (no CPU path in this library)")
-    x = x.contiguous()
-    if x.numel() != A * B * C:
-        raise ValueError("sum: shape mismatch")
-    cfg = SumConfig(mean=bool(mean))
-    plan = make_sum_plan(A, B, C, cfg)
-    out = torch.empty((B,), dtype=torch.float32, device=x.device)
-    ws = _workspace(torch, plan.workspace_bytes, x.device)
-    stream = torch.cuda.current_stream(x.device).cuda_stream
-    code = repro_sum_fp32_ws(x.data_ptr(), out.data_ptr(), A, B, C, cfg, ws.data_ptr(),
-                             ws.numel(), stream)
-    _check(code, "sum")
-    return out
+    mean), for a float32 tensor x viewed as [A][B][C]: on its GPU on the current stream, or on
+    the CPU (same bits). Same arguments and checks as the reference binding
+    (bindings.cpp:69-91)."""
+    return _backend.exact_sum(x, int(A), int(B), int(C), bool(mean))
 
 
 def scan_finite(x, flag, op_id):
-    """Lowers flag[0] (an int32 GPU tensor) to op_id if x holds a NaN or infinity, on the
-    current stream, without synchronising (bindings.cpp:286-297, kernels.cu:8-20)."""
-    import torch
-
-    if x.dtype != torch.float32:
-        raise ValueError("x must be float32")
-    if not (x.is_cuda and flag.is_cuda) or flag.dtype != torch.int32:
-        raise ValueError("scan_finite: x and an int32 flag must be GPU tensors")
-    x = x.contiguous()
-    stream = torch.cuda.current_stream(x.device).cuda_stream
-    code = lib.rg_scan_finite(x.data_ptr(), flag.data_ptr(), x.numel(), int(op_id), stream)
-    _check(code, "finite scan")
+    """Lowers flag[0] (an int32 tensor on x's device) to op_id if x holds a NaN or infinity;
+    on the GPU it is queued on the current stream without synchronising (bindings.cpp:286-297,
+    kernels.cu:8-20)."""
+    _backend.scan_finite(x, flag, int(op_id))
 
 
 __all__ = ["SumConfig", "SumPlan", "make_sum_plan", "sum_plan_for_device", "repro_sum_fp32_ws",

@@ -16,12 +16,15 @@ def pytest_configure(config):
 
 
 def _ensure_built():
-    """Builds the HIP library and the oracle only if they are missing."""
-    lib = os.path.join(REPO, "bit_reproducible_training_amd", "librepro_gemm.so")
-    if not os.path.exists(lib):
-        from bit_reproducible_training_amd import _build
+    """Builds the HIP library, its PyTorch binding and the oracle only if they are missing."""
+    import importlib.util
 
-        _build.build()
+    path = os.path.join(REPO, "bit_reproducible_training_amd", "_build.py")
+    spec = importlib.util.spec_from_file_location("_rg_build", path)
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    if not (os.path.exists(build.LIB_PATH) and os.path.exists(build.binding_path())):
+        build.build()
     if not os.path.exists(os.path.join(REPO, "oracle", "liboracle.so")):
         from oracle import oracle  # noqa: F401  (builds on import when missing)
 

@@ -171,3 +171,34 @@ def test_finite_guard_names_first_nonfinite_operation(torch_gpu):
     with pytest.raises(FloatingPointError, match="probe weight"):
         g.check()
     g.reset()
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_linear_cpu_and_gpu_give_identical_bits(torch_gpu, S):
+    """The same Linear step on CPU tensors (the CPU implementation in the compiled binding) and
+    on GPU tensors (the MI355X kernels): forward, dX, dW and db bit for bit."""
+    torch = torch_gpu
+    torch.manual_seed(10 + S)
+    m, n_in, n_out = 192, 400, 120
+    cpu = rg.Linear(n_in, n_out)
+    gpu = rg.Linear(n_in, n_out).cuda()
+    with torch.no_grad():
+        gpu.weight.copy_(cpu.weight)
+        gpu.bias.copy_(cpu.bias)
+    x = torch.randn(m, n_in)
+    dy = torch.randn(m, n_out)
+    rg.set_slices(S)
+    try:
+        xc = x.clone().requires_grad_(True)
+        yc = cpu(xc)
+        yc.backward(dy)
+        note("linear cpu vs gpu", S)
+        xg = x.cuda().requires_grad_(True)
+        yg = gpu(xg)
+        yg.backward(dy.cuda())
+        torch.cuda.synchronize()
+    finally:
+        rg.set_slices(3)
+    for a, b in ((yc, yg), (xc.grad, xg.grad), (cpu.weight.grad, gpu.weight.grad),
+                 (cpu.bias.grad, gpu.bias.grad)):
+        assert torch.equal(a.detach().view(torch.int32), b.detach().cpu().view(torch.int32))

@@ -338,5 +338,8 @@ def test_torch_gemm_binding(torch_gpu):
     Wt = torch.from_numpy(W.reshape(fout, fin).T.copy()).cuda().t()
     Y2 = rg.gemm(tX, Wt, B_, fout, fin, False, True, 3)
     assert torch.equal(Y2.view(torch.int32), Y.view(torch.int32))
+    # CPU tensors run the CPU implementation: the same bits
+    Yc = rg.gemm(torch.from_numpy(X), torch.from_numpy(W), B_, fout, fin, False, True, 3)
+    assert torch.equal(Yc.view(torch.int32), Y.cpu().view(torch.int32))
     with pytest.raises(ValueError):
-        rg.gemm(torch.from_numpy(X), torch.from_numpy(W), B_, fout, fin, False, True, 3)
+        rg.gemm(torch.from_numpy(X), tW, B_, fout, fin, False, True, 3)

@@ -116,8 +116,8 @@ def test_torch_exact_sum_binding(torch_gpu):
     out = rg.exact_sum(x.cuda(), 512, 96, 1)
     want = O.exact_sum(x.numpy(), 512, 96, 1)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
-    with pytest.raises(ValueError):
-        rg.exact_sum(x, 512, 96, 1)            # CPU tensor: no CPU path
+    cpu = rg.exact_sum(x, 512, 96, 1)          # CPU tensor: the CPU implementation, same bits
+    assert np.array_equal(cpu.numpy().view(np.uint32), want.view(np.uint32))
     with pytest.raises(ValueError):
         rg.exact_sum(x.cuda(), 512, 95, 1)     # shape mismatch
 
