@@ -17,6 +17,9 @@ HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
 HIP_ERROR_NOT_SUPPORTED = 801
 
+# Size of the fixed device workspace of rg_gemm_fp32_noalloc (include/repro_gemm.h).
+NOALLOC_SCRATCH_BYTES = 128 << 20
+
 
 class rg_config(ctypes.Structure):
     _fields_ = [
@@ -84,6 +87,9 @@ _SIGNATURES = {
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.POINTER(rg_config), ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p, ctypes.c_void_p]),
+    "rg_gemm_fp32_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.POINTER(rg_config), ctypes.c_void_p]),
     "rg_gemm_fp32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.POINTER(rg_config), ctypes.c_void_p]),

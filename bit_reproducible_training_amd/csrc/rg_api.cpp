@@ -11,6 +11,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "repro_gemm.h"
 #include "rg_internal.h"
@@ -366,6 +367,41 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     return hipGetLastError();
 }
 
+// Workspace of rg_gemm_fp32_noalloc: a fixed array in device memory, one copy per GPU (each
+// GPU that loads the code object gets its own). Host code must never pass `scratch` itself to a
+// kernel or a copy: on the host the name is only a stand-in for the symbol. Its device address
+// on the current GPU comes from hipGetSymbolAddress, taken once per device and kept in
+// g_scratch.
+static __device__ __align__(256) unsigned char scratch[RG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    int err = hipSuccess;
+};
+ScratchSlot g_scratch[64];
+
+// The scratch array's address on the current device (looked up on the first call per device).
+int scratch_on_current_device(void** out) {
+    int dev = 0;
+    int e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    ScratchSlot& slot = g_scratch[dev];
+    std::call_once(slot.once, [&slot]() {
+        void* p = nullptr;
+        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        slot.ptr = slot.err == hipSuccess ? p : nullptr;
+    });
+    if (slot.err != hipSuccess) return slot.err;
+    *out = slot.ptr;
+    return hipSuccess;
+}
+
+}  // namespace
+
 }  // namespace rg
 
 extern "C" {
@@ -461,6 +497,19 @@ int rg_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N, int 
     return rg::gemm_launch(A, B, C, L, static_cast<char*>(workspace),
                            static_cast<hipStream_t>(stream), stage_events, rg::GemmOptions(),
                            rg::dense_addressing(L));
+}
+
+int rg_gemm_fp32_noalloc(const float* A, const float* B, float* C, int M, int N, int K,
+                         const rg_config* cfg, void* stream) {
+    if (!A || !B || !C) return hipErrorInvalidValue;
+    rg::Layout L;
+    int e = rg::layout_for_current_device(M, N, K, cfg, &L);
+    if (e != hipSuccess) return e;
+    if (L.total > RG_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    if ((e = rg::scratch_on_current_device(&ws)) != hipSuccess) return e;
+    return rg::gemm_launch(A, B, C, L, static_cast<char*>(ws), static_cast<hipStream_t>(stream),
+                           nullptr, rg::GemmOptions(), rg::dense_addressing(L));
 }
 
 int rg_make_plan_strided_batched(int M, int N, int K, int batch, const rg_config* cfg,

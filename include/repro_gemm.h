@@ -143,6 +143,20 @@ int rg_gemm_strided_batched_fp32_ws(const float* A, long long lda, long long str
                                     int batch, const rg_config* cfg, void* workspace,
                                     size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: rg_gemm_fp32_ws for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a fixed device array inside the library, RG_NOALLOC_SCRATCH_BYTES (128 MiB)
+ * on each GPU, held from the first call on that GPU until the process ends; this entry point
+ * calls no hipMalloc/hipFree and no allocating library routine. The caller passes A, B, C as
+ * for rg_gemm_fp32_ws. Returns 1 (invalid value) when the plan's workspace_bytes
+ * (rg_make_plan) exceeds RG_NOALLOC_SCRATCH_BYTES (4096^3 at S = 3 needs about 96 MiB), or
+ * for the arguments rg_gemm_fp32_ws rejects. Every call on one GPU uses that GPU's array:
+ * calls that overlap on one GPU (two streams, two host threads) race and must be ordered on
+ * one stream. Same bits as rg_gemm_fp32_ws. Asynchronous on `stream`. */
+#define RG_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int rg_gemm_fp32_noalloc(const float* A, const float* B, float* C, int M, int N, int K,
+                         const rg_config* cfg, void* stream);
+
 /* Diagnostic, no counterpart in the reference: the sustained int8 MFMA rate of the current
  * (gfx950) device in TOP/s, measured with a kernel that keeps its operands in registers
  * (no memory traffic) for about a millisecond. dense = 1: random operand bytes, the
