@@ -117,15 +117,51 @@ def make_normal(n):
     return A, B
 
 
+def host_cpus():
+    """What the host offers the CPU baseline: nproc (os.cpu_count()), the CPUs this process may
+    run on (sched_getaffinity), the cgroup CPU quota if one is set, and the CPU model."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["affinity"] = os.cpu_count()
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            info["cgroup_quota_cpus"] = round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    try:
+        info["model"] = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                             if l.startswith("model name"))
+    except (OSError, StopIteration):
+        info["model"] = "unknown"
+    return info
+
+
+def default_cpu_threads(info):
+    """REPRO_CPU_THREADS if set (the reference's override, repro_gemm_cpu.h:14-23), else every
+    CPU the process may run on (hardware_concurrency() as the reference uses it, bounded by the
+    affinity mask)."""
+    env = os.environ.get("REPRO_CPU_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, int(info.get("affinity") or info.get("nproc") or 1))
+
+
 # --------------------------------------------------------------------------------------
-# CPU baseline and bit-exactness check: the reference's own CPU path (oracle/_ref) or this
-# repository's port, used here as the timed baseline and as the checker only.
+# CPU baseline and bit-exactness check: this repository's C port of the reference's CPU path
+# (oracle/repro_oracle.c: the same three passes and thread pool, pinned bit for bit to the
+# reference's own CPU path in this container), or the reference's path itself where
+# oracle/_ref was built (never on the GPU box). Used here as the timed baseline and as the
+# checker only.
 # --------------------------------------------------------------------------------------
 def cpu_baseline(A, B, n, gpu_C, threads, reps, fixtures, gpu_adv=None):
     from oracle import oracle as O
 
-    os.environ["REPRO_CPU_THREADS"] = str(threads)
+    info = host_cpus()
     kind = "reference" if O.ref is not None else "port"
+    os.environ["REPRO_CPU_THREADS"] = str(threads)
     times = []
     C = None
     for _ in range(reps):
@@ -138,10 +174,6 @@ def cpu_baseline(A, B, n, gpu_C, threads, reps, fixtures, gpu_adv=None):
     t = statistics.median(times)
     match = bool(np.array_equal(C.view(np.uint32), gpu_C.view(np.uint32)))
     out_hash = "%016x" % O.fnv1a64(C)
-    try:
-        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except Exception:  # noqa: BLE001
-        model = "unknown"
     checks = {"gpu_bits_equal_cpu": match}
     if "bench.4096cube.normal" in fixtures and n == 4096:
         checks["cpu_hash_equals_fixture"] = out_hash == fixtures["bench.4096cube.normal"]
@@ -154,8 +186,9 @@ def cpu_baseline(A, B, n, gpu_C, threads, reps, fixtures, gpu_adv=None):
         "cores": threads,
         "kind": kind,
         "sample": "the full %d^3 S=3 GEMM on the headline inputs, wall clock incl. quantisation, "
-                  "median of %d runs; host cpu %s" % (n, reps, model),
+                  "median of %d runs, %d threads" % (n, reps, threads),
         "ms": round(t * 1e3, 2),
+        "host": info,
     }
     return base, checks, out_hash
 
@@ -585,6 +618,61 @@ def configs_mode(torch, rg, reps=10, warmup=3):
                       "cases": rows}))
 
 
+def _rel_error(C, ref):
+    """(relative Frobenius error, worst row) of C against ref over the finite differences, as
+    the reference's hash tool reports them (hash_repro_gemm.cu:171-188)."""
+    d = C.astype(np.float64) - ref
+    ok = np.isfinite(d)
+    d2 = np.where(ok, d * d, 0.0)
+    r2 = np.where(ok, ref * ref, 0.0)
+    row_e, row_r = d2.sum(axis=1), r2.sum(axis=1)
+    live = row_r > 0
+    worst = float(np.sqrt(row_e[live] / row_r[live]).max()) if live.any() else 0.0
+    return (float(np.sqrt(d2.sum() / r2.sum())) if r2.sum() > 0 else 0.0), worst
+
+
+def accuracy_mode(torch, rg):
+    """One JSON line: accuracy against FP64 of the GPU results for every input distribution of
+    the reference's hash tool at its default shape (256 x 256 x 1024) and S = 1, 2, 3 (bits
+    checked against the oracle), and of the 4096^3 headline GEMM, next to FP32 torch.matmul."""
+    from oracle import oracle as O
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    rows = []
+    M, N, K = 256, 256, 1024
+    for dist in O.HASH_DISTS:
+        A, B = O.gen_hash_inputs(M, N, K, 12345, dist)
+        with np.errstate(over="ignore", invalid="ignore"):
+            ref = A.astype(np.float64) @ B.astype(np.float64)
+        dA, dB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+        row = {"dist": dist, "M": M, "N": N, "K": K}
+        for S in (1, 2, 3):
+            C = rg.gemm(dA, dB, M, N, K, False, False, S).cpu().numpy()
+            want = O.cpu_gemm(A, B, M, N, K, 0, 0, S)
+            with np.errstate(over="ignore", invalid="ignore"):
+                tot, worst = _rel_error(C, ref)
+            row["S%d" % S] = {"rel_frobenius": tot, "worst_row": worst,
+                              "bits_equal_oracle": bool(np.array_equal(C.view(np.uint32), want.view(np.uint32)))}
+        with np.errstate(over="ignore", invalid="ignore"):
+            row["torch_fp32"] = _rel_error(torch.matmul(dA, dB).cpu().numpy(), ref)[0]
+        rows.append(row)
+    n = 4096
+    A, B = make_normal(n)
+    dA, dB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+    ref64 = torch.matmul(dA.double(), dB.double())
+    head = {"shape": "4096^3 N(0,1), bench inputs"}
+
+    def rel(C):
+        d = (C.double() - ref64)
+        return float(torch.sqrt((d * d).sum() / (ref64 * ref64).sum()))
+
+    for S in (1, 2, 3):
+        head["S%d" % S] = rel(rg.gemm(dA, dB, n, n, n, False, False, S))
+    head["torch_fp32"] = rel(torch.matmul(dA, dB))
+    print(json.dumps({"mode": "accuracy", "reference": "FP64 product", "hash_tool_dists": rows,
+                      "headline": head}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -593,7 +681,9 @@ def main():
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-adversarial", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="threads of the CPU baseline (default: REPRO_CPU_THREADS, else every CPU "
+                         "this process may run on)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--widened", action="store_true",
                     help="time the exact sum, convolutions, batched GEMM and Linear layer instead")
@@ -601,6 +691,9 @@ def main():
                     help="time the reference GPT-2 suite's 21 GEMMs (1024 tokens) instead")
     ap.add_argument("--configs", action="store_true",
                     help="time every GEMM of BASELINE configurations 2, 3 and 5 instead")
+    ap.add_argument("--accuracy", action="store_true",
+                    help="report accuracy against FP64 (the reference hash tool's distributions "
+                         "and the headline GEMM) instead")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 device-to-device copies of 256 MiB (a plain copy kernel of "
                          "known size, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -622,6 +715,11 @@ def main():
     if args.configs:
         configs_mode(torch, rg)
         return
+    if args.accuracy:
+        accuracy_mode(torch, rg)
+        return
+    if args.cpu_threads is None:
+        args.cpu_threads = default_cpu_threads(host_cpus())
     if args.widened:
         widened(torch, rg, cpu=not args.no_cpu, threads=args.cpu_threads)
         return

@@ -25,15 +25,18 @@ enum class Algo {
     TensorCore = RG_ALGO_TENSOR_CORE // MFMA contraction, block tile chosen for the shape
 };
 
+// Field names, order and defaults are the reference's (repro_gemm.cuh:32-41); the meaning of
+// each field on this GPU:
 struct Config {
-    int split_k = 1;        // >= 1. May be raised automatically to keep int32 sums exact.
-    int tile_m = 16;        // a supported MFMA block tile (128/64) forces it; else auto
-    int tile_n = 16;
-    int tile_k = 32;        // ignored
+    int split_k = 1;        // K-parts summed in int64; the planner may use more (int32 chunk
+                            // limit, or to fill the GPU); never changes a bit of C
+    int tile_m = 16;        // 64 or 128 (with tile_n) pins that MFMA block tile; other values
+    int tile_n = 16;        //   leave the choice to the planner
+    int tile_k = 32;        // not used
     Algo algo = Algo::Auto;
-    int slices = 3;         // S, 1..MAX_SLICES
-    bool trans_a = false;   // false: A is MxK row-major.  true: A is KxM row-major (use A^T)
-    bool trans_b = false;   // false: B is KxN row-major.  true: B is NxK row-major (use B^T)
+    int slices = 3;         // S in 1..MAX_SLICES: inputs rounded to 7*S-bit integers
+    bool trans_a = false;   // A stored K rows of M (op(A) = A^T) instead of M rows of K
+    bool trans_b = false;   // B stored N rows of K (op(B) = B^T) instead of K rows of N
 };
 
 struct Plan {

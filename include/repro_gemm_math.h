@@ -96,8 +96,10 @@ RG_HD inline float round_to_float(int64_t T, int E) {
     uint32_t sign = T < 0 ? 0x80000000u : 0u;
     uint64_t m = T < 0 ? (uint64_t)0 - (uint64_t)T : (uint64_t)T;
     int p = 63 - clz64(m);                      // leading bit of T * 2^E at 2^(p+E)
-    int shift = p - 23;                         // keep 24 significant bits...
-    if (-149 - E > shift) shift = -149 - E;     // ...and nothing below 2^-149
+    // Bits of m to drop: enough to leave a binary32 significand (p - 23), or more when the
+    // result lies in the subnormal range, whose last bit has the weight 2^-149.
+    int shift = p - 23;
+    if (-149 - E > shift) shift = -149 - E;
     uint64_t q;
     int ex;
     if (shift <= 0) {

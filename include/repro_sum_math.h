@@ -1,15 +1,19 @@
 #pragma once
-// Exact, order-independent float32 summation, callable from host and device code.
-// Replaces repro_sum_cuda/repro_sum_math.cuh (same namespace, names and results).
+// repro_sum_math.h -- host/device scalar arithmetic of the exact float32 sum (namespace
+// repro_sum; the names LIMBS, split_float, acc_add, normalize and finalize are those of
+// repro_sum_cuda/repro_sum_math.cuh, so callers of that header compile against this one).
 //
-// Every finite float32 is an integer multiple of 2^-149 below 2^128. A sum of up to
-// 2^31 - 1 of them is an integer below 2^308 in those units, held as LIMBS = 10 signed
-// 64-bit limbs of radix 2^32 (value = sum_l limb[l] * 2^(32 l - 149)). Integer addition is
-// exact and associative, so accumulators can be filled and merged in any order or
-// grouping. The result is the exact sum (or exact sum / divisor) rounded once to float32,
-// nearest-even: an exactly zero result is +0.0, a nonzero result below half the smallest
-// subnormal is a zero of its sign, overflow gives +-inf, a NaN or infinity among the
-// inputs gives NaN.
+// Representation: the sum is an integer count of the smallest subnormal, 2^-149. A float32
+// below 2^128 is a whole number of those units below 2^277, and the int64 limbs below hold it
+// in radix 2^32 (limb l weighs 2^(32 l - 149)); with LIMBS = 10 there is room for the carries
+// of 2^31 - 1 summands. Limbs are signed and may run ahead of their radix between
+// normalisations, so the additions can be done in any order, split and merged freely: the
+// value is a plain integer sum.
+//
+// Rounding (finalize): the integer, or the integer divided by a count for a mean, is rounded
+// to float32 once, nearest-even. Conventions: a zero result is +0.0; a nonzero result that
+// rounds to zero keeps its sign; a result beyond the float32 range is an infinity of its sign;
+// any NaN or infinity among the summands makes the result NaN.
 #include <cstdint>
 
 #include "repro_gemm_math.h"

@@ -35,6 +35,7 @@ _SIG = {
     "oracle_gen_uniform": (None, [_vp, _sz, _d, _u64]),
     "oracle_gen_uniform_pm": (None, [_vp, _sz, _f, _u64, _u64]),
     "oracle_gen_adversarial": (None, [_vp, _i, _i, _u64, _i, _i]),
+    "oracle_gen_hash_inputs": (_i, [_vp, _vp, _i, _i, _i, _u64, _i]),
     "oracle_splitmix64": (None, [_vp, _sz, _u64]),
     "oracle_fnv1a64": (_u64, [_vp, _sz, _u64]),
     "oracle_exact_sum": (None, [_vp, _vp, _i, _i, _i, _i]),
@@ -109,6 +110,19 @@ def gen_uniform_pm(n, bound, seed, first=0):
     out = np.empty(int(n), np.float32)
     lib.oracle_gen_uniform_pm(_ptr(out), out.size, float(bound), int(seed), int(first))
     return out
+
+
+HASH_DISTS = ("uniform", "normal", "weights", "wide", "stress")
+
+
+def gen_hash_inputs(M, N, K, seed, dist):
+    """A [M][K], B [K][N] as the reference's hash tool draws them for `dist` (one of HASH_DISTS,
+    hash_repro_gemm.cu:20-56)."""
+    A = np.empty((int(M), int(K)), np.float32)
+    B = np.empty((int(K), int(N)), np.float32)
+    assert lib.oracle_gen_hash_inputs(_ptr(A), _ptr(B), int(M), int(N), int(K), int(seed),
+                                      HASH_DISTS.index(dist)) == 0
+    return A, B
 
 
 def gen_adversarial(rows, cols, seed, pair_rows=False, negate=False):

@@ -461,6 +461,70 @@ void oracle_gen_uniform(float* out, size_t n, double scale, uint64_t seed) {
 void oracle_gen_uniform_pm(float* out, size_t n, float bound, uint64_t seed, uint64_t first_elem) {
     gen_run(out, n, (double)bound, seed, first_elem, GEN_UNIFORM_PM, 0);
 }
+/* The input distributions of the reference's hash tool (repro_gemm_cuda/hash_repro_gemm.cu:20-56),
+ * drawn in its order from one sequential SplitMix64 stream with the Rng helpers of
+ * repro_test_util.h:29-47: u01 = (next >> 40) 2^-24; normal = sum of 12 u01 - 6 in double;
+ * range(lo, hi) = lo + next % (hi - lo + 1); wide(lo, hi) = +-(1 + u01) 2^range(lo, hi), the
+ * sign from the next draw's low bit. A is MxK, B is KxN, row-major. dist: 0 uniform U[-1,1),
+ * 1 normal, 2 weights (0.02 normal, x100 when the following draw % 1000 == 0), 3 wide
+ * (2^[-40,40]), 4 stress (normal, then rows of A by r % 8 and columns of B by c % 6 replaced by
+ * zeros, subnormals, 1e30-scaled values, one 1e6 outlier, signed zeros, 2^[-60,60] values or
+ * 2^-120-scaled values). */
+typedef struct { uint64_t s; } seq_rng;
+static uint64_t seq_next(seq_rng* g) { g->s += 0x9e3779b97f4a7c15ull; return sm_mix(g->s); }
+static double seq_u01(seq_rng* g) { return (double)(seq_next(g) >> 40) * (1.0 / 16777216.0); }
+static double seq_normal(seq_rng* g) {
+    double t = 0.0;
+    for (int i = 0; i < 12; ++i) t += seq_u01(g);
+    return t - 6.0;
+}
+static int seq_range(seq_rng* g, int lo, int hi) { return lo + (int)(seq_next(g) % (uint64_t)(hi - lo + 1)); }
+static float seq_wide(seq_rng* g, int lo, int hi) {
+    double mant = 1.0 + seq_u01(g);
+    double v = ldexp(mant, seq_range(g, lo, hi));
+    return (float)((seq_next(g) & 1) ? -v : v);
+}
+static float seq_dist(seq_rng* g, int dist) {
+    switch (dist) {
+        case 0: return (float)(2.0 * seq_u01(g) - 1.0);
+        case 2: {
+            double v = 0.02 * seq_normal(g);
+            return (float)((seq_next(g) % 1000 == 0) ? v * 100.0 : v);
+        }
+        case 3: return seq_wide(g, -40, 40);
+        default: return (float)seq_normal(g);
+    }
+}
+
+int oracle_gen_hash_inputs(float* A, float* B, int M, int N, int K, uint64_t seed, int dist) {
+    if (dist < 0 || dist > 4 || M <= 0 || N <= 0 || K <= 0) return 1;
+    seq_rng g = {seed};
+    size_t nA = (size_t)M * K, nB = (size_t)K * N;
+    for (size_t i = 0; i < nA; ++i) A[i] = seq_dist(&g, dist);
+    for (size_t i = 0; i < nB; ++i) B[i] = seq_dist(&g, dist);
+    if (dist != 4) return 0;
+    for (int r = 0; r < M; ++r) {
+        float* row = A + (size_t)r * K;
+        switch (r % 8) {
+            case 1: for (int k = 0; k < K; ++k) row[k] = 0.0f; break;
+            case 2: for (int k = 0; k < K; ++k) row[k] = (float)ldexp(seq_normal(&g), -140); break;
+            case 3: for (int k = 0; k < K; ++k) row[k] = (float)(1e30 * seq_normal(&g)); break;
+            case 4: row[seq_range(&g, 0, K - 1)] = 1e6f; break;
+            case 5: for (int k = 0; k < K; ++k) row[k] = (k & 1) ? -0.0f : 0.0f; break;
+            default: break;
+        }
+    }
+    for (int c = 0; c < N; ++c) {
+        switch (c % 6) {
+            case 1: for (int k = 0; k < K; ++k) B[(size_t)k * N + c] = 0.0f; break;
+            case 2: for (int k = 0; k < K; ++k) B[(size_t)k * N + c] = seq_wide(&g, -60, 60); break;
+            case 3: for (int k = 0; k < K; ++k) B[(size_t)k * N + c] = (float)ldexp(seq_normal(&g), -120); break;
+            default: break;
+        }
+    }
+    return 0;
+}
+
 void oracle_gen_adversarial(float* out, int rows, int cols, uint64_t seed, int pair_rows, int negate) {
     gen_ctx g;
     memset(&g, 0, sizeof g);

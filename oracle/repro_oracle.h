@@ -104,6 +104,9 @@ void oracle_gen_uniform_pm(float* out, size_t n, float bound, uint64_t seed, uin
  * when negate is set, so negated pairs in op(A) against plain pairs in op(B) cancel
  * almost exactly in every dot product. */
 void oracle_gen_adversarial(float* out, int rows, int cols, uint64_t seed, int pair_rows, int negate);
+/* hash_repro_gemm.cu:20-56 input distributions (0 uniform, 1 normal, 2 weights, 3 wide, 4 stress)
+ * from one sequential stream; returns 1 for a bad argument. */
+int oracle_gen_hash_inputs(float* A, float* B, int M, int N, int K, uint64_t seed, int dist);
 /* Raw stream: n successive SplitMix64 outputs. */
 void oracle_splitmix64(uint64_t* out, size_t n, uint64_t seed);
 

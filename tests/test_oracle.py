@@ -6,6 +6,7 @@ with Python integers, the reference's recorded suite hashes, and the reference's
 path compiled from its headers (oracle/_ref) where that is built.
 """
 import json
+import math
 import os
 import random
 
@@ -357,3 +358,97 @@ def test_baseline_fixtures_small_configs():
         assert "%016x" % O.fnv_chain(A, B) == row["in_hash"]
         C = O.cpu_gemm(A, B, case["M"], case["N"], case["K"], case["ta"], case["tb"], case["S"])
         assert "%016x" % O.fnv1a64(C) == row["out_hash"]
+
+
+class _PyStream:
+    """The hash tool's sequential Rng (repro_test_util.h:29-47) in Python integers and floats."""
+
+    def __init__(self, seed):
+        self.draws = iter(_py_splitmix(seed, 1 << 20))
+
+    def next(self):
+        return next(self.draws)
+
+    def u01(self):
+        return (self.next() >> 40) * (1.0 / 16777216.0)
+
+    def normal(self):
+        t = 0.0
+        for _ in range(12):
+            t += self.u01()
+        return t - 6.0
+
+    def range(self, lo, hi):
+        return lo + self.next() % (hi - lo + 1)
+
+    def wide(self, lo, hi):
+        mant = 1.0 + self.u01()
+        v = math.ldexp(mant, self.range(lo, hi))
+        return np.float32(-v if self.next() & 1 else v)
+
+
+def _py_hash_inputs(M, N, K, seed, dist):
+    g = _PyStream(seed)
+
+    def one():
+        if dist == "uniform":
+            return np.float32(2.0 * g.u01() - 1.0)
+        if dist == "weights":
+            v = 0.02 * g.normal()
+            return np.float32(v * 100.0 if g.next() % 1000 == 0 else v)
+        if dist == "wide":
+            return g.wide(-40, 40)
+        return np.float32(g.normal())
+
+    A = np.array([one() for _ in range(M * K)], np.float32).reshape(M, K)
+    B = np.array([one() for _ in range(K * N)], np.float32).reshape(K, N)
+    if dist == "stress":
+        for r in range(M):
+            m = r % 8
+            if m == 1:
+                A[r] = 0.0
+            elif m == 2:
+                A[r] = [np.float32(math.ldexp(g.normal(), -140)) for _ in range(K)]
+            elif m == 3:
+                A[r] = [np.float32(1e30 * g.normal()) for _ in range(K)]
+            elif m == 4:
+                A[r, g.range(0, K - 1)] = 1e6
+            elif m == 5:
+                A[r] = [-0.0 if k & 1 else 0.0 for k in range(K)]
+        for c in range(N):
+            m = c % 6
+            if m == 1:
+                B[:, c] = 0.0
+            elif m == 2:
+                B[:, c] = [g.wide(-60, 60) for _ in range(K)]
+            elif m == 3:
+                B[:, c] = [np.float32(math.ldexp(g.normal(), -120)) for _ in range(K)]
+    return A, B
+
+
+@pytest.mark.parametrize("dist", O.HASH_DISTS)
+def test_hash_tool_distributions_match_python_stream(dist):
+    """oracle_gen_hash_inputs against a Python restatement of the same sequential stream, bit
+    for bit, and the properties each distribution promises (hash_repro_gemm.cu:13-17). The
+    reference records no outputs of these distributions, so the exact input bits are pinned
+    only by SplitMix64's known answer and this second implementation; GPU parity does not
+    depend on them (the GPU and the oracle see the same inputs)."""
+    for M, N, K, seed in ((5, 7, 9, 12345), (16, 6, 24, 99)):
+        A, B = O.gen_hash_inputs(M, N, K, seed, dist)
+        PA, PB = _py_hash_inputs(M, N, K, seed, dist)
+        assert np.array_equal(A.view(np.uint32), PA.view(np.uint32)), dist
+        assert np.array_equal(B.view(np.uint32), PB.view(np.uint32)), dist
+    A, B = O.gen_hash_inputs(64, 48, 200, 7, dist)
+    v = np.concatenate([A.ravel(), B.ravel()])
+    assert np.isfinite(v).all()
+    if dist == "uniform":
+        assert v.min() >= -1.0 and v.max() < 1.0
+    elif dist == "wide":
+        e = np.frexp(np.abs(v).astype(np.float64))[1] - 1
+        assert e.min() >= -40 and e.max() <= 40 and e.max() - e.min() > 60
+    elif dist == "weights":
+        big = np.abs(v) > 0.5
+        assert 0 < big.sum() < 0.01 * v.size       # the rare x100 outliers
+    elif dist == "stress":
+        assert (A[1] == 0).all() and (np.abs(A[2]) < 2.0 ** -126).all() and np.abs(A[3]).max() > 1e29
+        assert (A[5].view(np.uint32)[1::2] == 0x80000000).all() and (B[:, 1] == 0).all()
