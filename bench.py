@@ -562,11 +562,13 @@ def _config_cases():
     return cases
 
 
-def configs_mode(torch, rg, reps=10, warmup=3):
-    """One JSON line: every GEMM of BASELINE configurations 2, 3 and 5 timed on the GPU (HIP
-    events around `reps` back-to-back GEMMs after `warmup`), its effective FP32 TFLOP/s, the
-    contraction's share of the dense int8 MFMA peak (stage events, a second pass), the plan,
-    and whether two runs gave identical bits."""
+def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
+    """One JSON line: every GEMM of BASELINE configurations 2, 3 and 5 timed on the GPU in steady
+    state: back-to-back GEMMs for about `warm_ms` of GPU time (past the GPU's power-management
+    transient after a change of load), then HIP events around about `timed_ms` of back-to-back
+    GEMMs (at least 10). Reports effective FP32 TFLOP/s, the stage times (median of 5 runs with
+    stage events: slicing, contraction, final rounding), the contraction's share of the dense
+    int8 MFMA peak, the plan, and whether the runs gave identical bits."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2024)
     sp = torch.cuda.current_stream().cuda_stream
@@ -588,10 +590,16 @@ def configs_mode(torch, rg, reps=10, warmup=3):
             if code != 0:
                 raise rg.ReproGemmError(code, name)
 
-        for _ in range(warmup):
-            step()
-        first = C.clone()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step()
+        e1.record()
+        torch.cuda.synchronize()
+        once = max(e0.elapsed_time(e1), 1e-3)
+        first = C.clone()
+        for _ in range(max(3, int(warm_ms / once))):
+            step()
+        reps = max(10, int(timed_ms / once))
         e0.record()
         for _ in range(reps):
             step()
@@ -602,13 +610,17 @@ def configs_mode(torch, rg, reps=10, warmup=3):
         for e in evs:
             e.record()
         torch.cuda.synchronize()
-        step([e.cuda_event for e in evs])
-        torch.cuda.synchronize()
-        contract_ms = evs[1].elapsed_time(evs[2])
+        stages = []
+        for _ in range(5):
+            step([e.cuda_event for e in evs])
+            torch.cuda.synchronize()
+            stages.append([evs[i].elapsed_time(evs[i + 1]) for i in range(3)])
+        slice_ms, contract_ms, final_ms = (statistics.median(x[i] for x in stages) for i in range(3))
         flops = 2.0 * M * N * K
         rows.append({"case": name, "M": M, "N": N, "K": K, "ta": ta, "tb": tb, "S": S,
-                     "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-                     "contract_ms": round(contract_ms, 4),
+                     "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "reps": reps,
+                     "slice_ms": round(slice_ms, 4), "contract_ms": round(contract_ms, 4),
+                     "final_ms": round(final_ms, 4),
                      "contract_int8_frac": round(S * S * flops / (contract_ms * 1e-3) / (PEAK_INT8_TOPS * 1e12), 4),
                      "plan": "%dx%d split %d" % (plan.tile_m, plan.tile_n, plan.split_k),
                      "repeat_bits_equal": bool(torch.equal(first.view(torch.int32), C.view(torch.int32)))})

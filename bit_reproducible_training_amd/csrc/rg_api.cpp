@@ -72,9 +72,10 @@ void choose_chunks(int R, int rows, int K, bool strided, int* nch, int* kch) {
 // block slots (compute units x blocks resident per compute unit, from the block's LDS ring);
 // a block costs a fixed prologue/epilogue plus one pipeline stage per 64 values of k of its
 // part; a split adds the int64 partials' traffic (written once, read once) at about 4 TB/s.
-// Constants are fitted to MI355X measurements of the 128x128 and 64x64 kernels at S = 3
-// (1.75 us per 128x128 stage, 1.0 us per 64x64 stage with two blocks per compute unit) and
-// scaled by the MFMA work per stage, S^2, for fewer slices.
+// Constants are fitted to MI355X measurements of every block tile x split on 22 shapes (the
+// GPT-2 and LM-head GEMMs of the BASELINE configurations, squares, tall and long-K shapes; the
+// plan picked is the fastest measured, or within 7% of it) at S = 3, and scaled by the MFMA work
+// per stage, S^2, for fewer slices.
 // Blocks of one MFMA tile resident per compute unit: the LDS ring (3 stages of the block's
 // digit panels) against 160 KiB, at most 2.
 int blocks_per_cu(int ti, int tj, int S) {
@@ -89,8 +90,8 @@ double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split,
     const double slots = (double)std::max(1, num_cus) * per_cu;
     const double waves = std::ceil(tiles * split / slots);
     const double w = ti * tj / 4.0;  // work of a block stage relative to the 128x128 tile
-    const double stage_us = 0.2 + 1.55 * w * per_cu * (S * S / 9.0);
-    const double fixed_us = 2.0 + 8.0 * w * per_cu;
+    const double stage_us = 0.1 + 1.4 * w * per_cu * (S * S / 9.0);
+    const double fixed_us = 1.0 + 4.0 * w * per_cu;
     const double steps = std::ceil((double)nsteps / split);
     double t = waves * (steps * stage_us + fixed_us);
     if (split > 1 || raw) {
