@@ -630,6 +630,65 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
                       "cases": rows}))
 
 
+SWEEP_SHAPES = [("sq4096", 4096, 4096, 4096, 0, 0), ("sq2048", 2048, 2048, 2048, 0, 0),
+                ("sq1024", 1024, 1024, 1024, 0, 0), ("r512x512x8192", 512, 512, 8192, 0, 0),
+                ("r4096x1024x1024", 4096, 1024, 1024, 0, 1), ("r16384x1024x4096", 16384, 1024, 4096, 0, 0),
+                ("r2048x8192x1024", 2048, 8192, 1024, 0, 0)]
+
+
+def sweep_plans(torch, rg, warm_ms=15.0, timed_ms=15.0):
+    """One JSON line per shape: every block tile (128x128, 128x64, 64x128, 64x64) x split_k in
+    {1, 2, 3, 4, 6, 8, 12, 16} forced through Config, each timed over about `timed_ms` of
+    back-to-back GEMMs after about `warm_ms` (S = 3), next to the plan the planner picks. The
+    data the planner's cost model (rg_api.cpp::plan_cost) is fitted to."""
+    cases = [(c[0], c[1], c[2], c[3], c[4], c[5]) for c in _config_cases() if c[0].startswith(("c3", "c5"))]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2024)
+    sp = torch.cuda.current_stream().cuda_stream
+    for name, M, N, K, ta, tb in cases + SWEEP_SHAPES:
+        dA = torch.randn(M * K, device="cuda", generator=gen)
+        dB = torch.randn(K * N, device="cuda", generator=gen)
+        C = torch.empty((M, N), device="cuda")
+        auto = rg.make_plan(M, N, K, rg.Config(trans_a=ta, trans_b=tb))
+        res, seen = [], set()
+        for tm, tn in ((128, 128), (128, 64), (64, 128), (64, 64)):
+            for split in (1, 2, 3, 4, 6, 8, 12, 16):
+                cfg = rg.Config(trans_a=ta, trans_b=tb, tile_m=tm, tile_n=tn, split_k=split)
+                plan = rg.make_plan(M, N, K, cfg)
+                if (tm, tn, plan.split_k) in seen:
+                    continue
+                seen.add((tm, tn, plan.split_k))
+                ws = torch.empty(max(plan.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
+
+                def step():
+                    code = rg.repro_gemm_fp32_ws(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), M, N, K,
+                                                 cfg, ws.data_ptr(), ws.numel(), sp, None)
+                    if code != 0:
+                        raise rg.ReproGemmError(code, name)
+
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                step()
+                e1.record()
+                torch.cuda.synchronize()
+                once = max(e0.elapsed_time(e1), 1e-3)
+                for _ in range(max(5, int(warm_ms / once))):
+                    step()
+                n = max(10, int(timed_ms / once))
+                e0.record()
+                for _ in range(n):
+                    step()
+                e1.record()
+                torch.cuda.synchronize()
+                res.append([tm, tn, plan.split_k, round(e0.elapsed_time(e1) / n, 4)])
+                del ws
+        print(json.dumps({"mode": "sweep_plans", "case": name, "M": M, "N": N, "K": K, "ta": ta,
+                          "tb": tb, "auto": [auto.tile_m, auto.tile_n, auto.split_k], "res": res}),
+              flush=True)
+        del dA, dB, C
+        torch.cuda.empty_cache()
+
+
 def _rel_error(C, ref):
     """(relative Frobenius error, worst row) of C against ref over the finite differences, as
     the reference's hash tool reports them (hash_repro_gemm.cu:171-188)."""
@@ -703,6 +762,8 @@ def main():
                     help="time the reference GPT-2 suite's 21 GEMMs (1024 tokens) instead")
     ap.add_argument("--configs", action="store_true",
                     help="time every GEMM of BASELINE configurations 2, 3 and 5 instead")
+    ap.add_argument("--sweep-plans", action="store_true",
+                    help="time every block tile x split on the planner's fitting shapes instead")
     ap.add_argument("--accuracy", action="store_true",
                     help="report accuracy against FP64 (the reference hash tool's distributions "
                          "and the headline GEMM) instead")
@@ -729,6 +790,9 @@ def main():
         return
     if args.accuracy:
         accuracy_mode(torch, rg)
+        return
+    if args.sweep_plans:
+        sweep_plans(torch, rg)
         return
     if args.cpu_threads is None:
         args.cpu_threads = default_cpu_threads(host_cpus())
