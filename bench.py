@@ -542,7 +542,7 @@ def widened(torch, rg, cpu=True, threads=16):
 # which the GPU tests check against the CPU oracle's hashes. Here: (name, M, N, K, ta, tb, S,
 # scale of A, scale of B) with inputs drawn on the GPU (torch.randn, uniform for LeNet weights).
 def _config_cases():
-    cases = []
+    cases = [("c1.256cube", 256, 256, 256, 0, 0, 3, 1.0, 1.0)]
     for li, (fin, fout) in enumerate([(400, 120), (120, 84), (84, 10)]):
         u = 1.0 / (fin ** 0.5)
         for S in (1, 2, 3):
@@ -562,13 +562,40 @@ def _config_cases():
     return cases
 
 
+def _graph_ms(torch, step, reps=20):
+    """GPU time per call of `step`: `reps` calls captured in one HIP graph and replayed, so the
+    host's launch cost (a ctypes call and the launches, about 8 us) is not in the figure."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(stream=side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            step(stream=torch.cuda.current_stream().cuda_stream)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / (5 * reps)
+
+
 def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
-    """One JSON line: every GEMM of BASELINE configurations 2, 3 and 5 timed on the GPU in steady
-    state: back-to-back GEMMs for about `warm_ms` of GPU time (past the GPU's power-management
-    transient after a change of load), then HIP events around about `timed_ms` of back-to-back
-    GEMMs (at least 10). Reports effective FP32 TFLOP/s, the stage times (median of 5 runs with
-    stage events: slicing, contraction, final rounding), the contraction's share of the dense
-    int8 MFMA peak, the plan, and whether the runs gave identical bits."""
+    """One JSON line: every GEMM of BASELINE configurations 1, 2, 3 and 5 timed on the GPU in
+    steady state: back-to-back GEMMs for about `warm_ms` of GPU time (past the GPU's
+    power-management transient after a change of load), then HIP events around about `timed_ms`
+    of back-to-back GEMMs (at least 10). Reports effective FP32 TFLOP/s, the stage times (median of
+    5 runs with stage events: slicing, contraction, final rounding), the contraction's share of the
+    dense int8 MFMA peak, the plan, and whether the runs gave identical bits. GEMMs of less than
+    0.1 ms also get `graph_ms`, the GPU time per GEMM without the host's launch cost."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2024)
     sp = torch.cuda.current_stream().cuda_stream
@@ -584,9 +611,9 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
         ws = torch.empty(max(plan.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
         C = torch.empty((M, N), dtype=torch.float32, device="cuda")
 
-        def step(events=None):
+        def step(events=None, stream=sp):
             code = rg.repro_gemm_fp32_ws(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), M, N, K, cfg,
-                                         ws.data_ptr(), ws.numel(), sp, events)
+                                         ws.data_ptr(), ws.numel(), stream, events)
             if code != 0:
                 raise rg.ReproGemmError(code, name)
 
@@ -616,9 +643,11 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
             torch.cuda.synchronize()
             stages.append([evs[i].elapsed_time(evs[i + 1]) for i in range(3)])
         slice_ms, contract_ms, final_ms = (statistics.median(x[i] for x in stages) for i in range(3))
+        graph_ms = round(_graph_ms(torch, step), 4) if ms < 0.1 else None
         flops = 2.0 * M * N * K
         rows.append({"case": name, "M": M, "N": N, "K": K, "ta": ta, "tb": tb, "S": S,
                      "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "reps": reps,
+                     "graph_ms": graph_ms,
                      "slice_ms": round(slice_ms, 4), "contract_ms": round(contract_ms, 4),
                      "final_ms": round(final_ms, 4),
                      "contract_int8_frac": round(S * S * flops / (contract_ms * 1e-3) / (PEAK_INT8_TOPS * 1e12), 4),

@@ -101,6 +101,23 @@ double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split,
     return t;
 }
 
+// The one-launch small-shape kernel (contract_small): for plain GEMMs with the default split and
+// no pinned 64/128 tile (RG_ALGO_TILED pins 64x64), K within its LDS panels, and either a pinned
+// 32x32 tile or at most one block per compute unit. Measured on MI355X (GPU time per GEMM, S = 3):
+// 256^3 7.7 us against 12.1 us for the two-launch pipeline, the LeNet layers 5.6-8.4 us against
+// 7.4-10.0 us, 512x512x512 (256 tiles) 10.5 against 12.0 us; with four blocks per compute unit
+// (1024x1024x64) it takes 20 us against 8.4 us, so more tiles than compute units keep the
+// pipeline.
+bool small_path(int M, int N, int K, int batch, int split_k, int tile_m, int tile_n, int algo,
+                const PlanExtras& extras, int num_cus) {
+    if (algo == RG_ALGO_TILED || split_k != 1 || K > SMALL_MAX_K) return false;
+    if (!extras.one_launch || extras.raw || !extras.gemm_bound) return false;
+    if (tile_m == 32 && tile_n == 32) return true;
+    if ((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128)) return false;
+    const double tiles = (double)ceil_div(M, 32) * ceil_div(N, 32) * batch;
+    return tiles <= std::max(1, num_cus);
+}
+
 }  // namespace
 
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
@@ -136,6 +153,18 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
     } else {
         if (!dev.gfx950) return hipErrorNotSupported;
         L.algo = algo == RG_ALGO_TILED ? RG_ALGO_TILED : RG_ALGO_TENSOR_CORE;
+        if (small_path(M, N, K, batch, split_k, tile_m, tile_n, algo, extras, dev.num_cus)) {
+            L.small = true;
+            L.Mp = round_up(M, PANEL_ROWS);
+            L.Np = round_up(N, PANEL_ROWS);
+            L.split = 1;
+            L.has_partial = false;
+            // Nothing of the workspace is used; a non-empty one keeps the callers' contract
+            // (a workspace of at least the planned size) the same for every plan.
+            L.total = 256;
+            *Lp = L;
+            return hipSuccess;
+        }
         const int nsteps = L.Kp / STEP_K;
         const int min_split = ceil_div(nsteps, max_steps_per_part(S));
         // Candidate block tiles: the forced one, or 128x128 and 64x64; candidate splits: the
@@ -276,6 +305,17 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     auto record = [&](int i) {
         if (stage_events) (void)hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream);
     };
+    if (L.small) {  // slicing, contraction and rounding in one kernel
+        if (opt.group_a > 0 || opt.group_b > 0 || opt.raw || opt.im2col_a || !A ||
+            L.K > SMALL_MAX_K)
+            return hipErrorInvalidValue;
+        record(0);
+        record(1);
+        launch_contract_small(L, A, B, C, addr, stream);
+        record(2);
+        record(3);
+        return hipGetLastError();
+    }
     void* qa = base + L.qa;
     void* qb = base + L.qb;
     int* ea = reinterpret_cast<int*>(base + L.ea);
@@ -427,8 +467,8 @@ int rg_make_plan(int M, int N, int K, const rg_config* cfg, rg_plan* plan) {
     plan->algo = L.algo;
     plan->split_k = L.split;
     plan->workspace_bytes = L.total;
-    plan->tile_m = 64 * L.ti;
-    plan->tile_n = 64 * L.tj;
+    plan->tile_m = L.small ? 32 : 64 * L.ti;
+    plan->tile_n = L.small ? 32 : 64 * L.tj;
     return hipSuccess;
 }
 
@@ -443,8 +483,8 @@ int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950,
     plan->algo = L.algo;
     plan->split_k = L.split;
     plan->workspace_bytes = L.total;
-    plan->tile_m = 64 * L.ti;
-    plan->tile_n = 64 * L.tj;
+    plan->tile_m = L.small ? 32 : 64 * L.ti;
+    plan->tile_n = L.small ? 32 : 64 * L.tj;
     if (info) {
         info->qa = L.qa;
         info->qb = L.qb;
@@ -524,8 +564,8 @@ int rg_make_plan_strided_batched(int M, int N, int K, int batch, const rg_config
     plan->algo = L.algo;
     plan->split_k = L.split;
     plan->workspace_bytes = L.total;
-    plan->tile_m = 64 * L.ti;
-    plan->tile_n = 64 * L.tj;
+    plan->tile_m = L.small ? 32 : 64 * L.ti;
+    plan->tile_n = L.small ? 32 : 64 * L.tj;
     return hipSuccess;
 }
 

@@ -391,6 +391,190 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #endif
 }
 
+// One-launch GEMM for small shapes (K <= SMALL_MAX_K): a block of 16 wavefronts owns a 32x32
+// tile of C and does every step of the definition for it. Its 32 rows of op(A) and 32 columns
+// of op(B) are cut into slots of 16 consecutive k of one row (the 16 bytes one lane contributes
+// to a digit panel); each thread loads its slots' values into registers at once (one memory
+// latency for the block), takes their maxima into the rows' maxima (LDS atomics on the
+// non-negative floats' bit patterns, which order as the values do), and after the exponents
+// rounds them to fixed point and writes their digits into LDS panels. Wavefront w < 4 contracts
+// k panels w, w + 4, ... with V_MFMA_I32_32X32X32_I8; the four wavefronts' level sums are added
+// in LDS and every output is rounded once. Sixteen wavefronts (four per SIMD) keep the code
+// short (two slots per thread) and hide the latency of the rounding's dependent instructions. Neighbouring tiles round the same rows again; for
+// shapes this small that costs less than the slicing launch it replaces. The values and integer
+// sums are the pipeline's, so are the bits.
+// Operand o (0: op(A), row r = tile row; 1: op(B), row r = tile column) has element (r, k) at
+// src[r * ld + k] (row access) or src[k * ld + r] (strided); vec: row access with 16-byte
+// aligned rows and K % 4 == 0.
+struct SmallOperand {
+    const float* src;
+    long long ld;
+    int R;        // rows of op(X) (M or N)
+    int strided;
+    int vec;
+};
+
+constexpr int SMALL_THREADS = 1024;
+constexpr int SMALL_SLOTS = 2 * (SMALL_MAX_K / PANEL_K) * 64 / SMALL_THREADS;  // per thread, at most
+
+template <int S>
+struct SmallLds {
+    static constexpr int PANELS = 2 * S * (SMALL_MAX_K / PANEL_K);  // digit panels of both operands
+    static constexpr int RED = 4 * (2 * S - 1) * 16;                 // 64-lane int rows of the sums
+    static constexpr int V4 = (PANELS * 64 > RED * 16 ? PANELS * 64 : RED * 16);  // in v4i
+};
+
+template <int S>
+__global__ void __launch_bounds__(SMALL_THREADS, 1)
+contract_small(SmallOperand a, SmallOperand b, float* __restrict__ C, int K, long long ldc,
+               long long stride_a, long long stride_b, long long stride_c, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int L = 2 * S - 1;
+    __shared__ v4i buf[SmallLds<S>::V4];
+    __shared__ int rmax[2][32];   // bit patterns of the rows' maxima
+    __shared__ int sexp[2][32];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int npk = (K + PANEL_K - 1) / PANEL_K;
+    const int slots = 2 * npk * 64;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+    const int item = blockIdx.z;
+    a.src += (size_t)item * stride_a;
+    b.src += (size_t)item * stride_b;
+    C += (size_t)item * stride_c;
+    const int r0[2] = {tm * 32, tn * 32};
+    if (t < 64) rmax[t >> 5][t & 31] = 0;
+    __syncthreads();
+
+    // Slot i = t + SMALL_THREADS j: operand o = i / (64 npk), k panel kp, lane s of the panel: row s % 32,
+    // k = 32 kp + 16 (s / 32) .. + 15. Every load of every slot is issued before any is used.
+    float x[SMALL_SLOTS][16];
+#pragma unroll
+    for (int j = 0; j < SMALL_SLOTS; ++j) {
+        const int i = t + SMALL_THREADS * j;
+        const int o = i >= npk * 64 ? 1 : 0;
+        const int rem = i - o * npk * 64;
+        const int kp = rem >> 6, s = rem & 63;
+        const int r = r0[o] + (s & 31), k0 = kp * PANEL_K + 16 * (s >> 5);
+        const SmallOperand& op = o == 0 ? a : b;
+        const bool live = i < slots && r < op.R;
+        if (live && op.vec) {
+            const float4* p = reinterpret_cast<const float4*>(op.src + (size_t)r * op.ld + k0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (k0 + 4 * q < K) v = p[q];  // K % 4 == 0: a float4 is wholly in or out
+                x[j][4 * q] = v.x;
+                x[j][4 * q + 1] = v.y;
+                x[j][4 * q + 2] = v.z;
+                x[j][4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int k = k0 + e;
+                x[j][e] = 0.0f;
+                if (live && k < K)
+                    x[j][e] = op.strided ? op.src[(size_t)k * op.ld + r] : op.src[(size_t)r * op.ld + k];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < SMALL_SLOTS; ++j) {
+        const int i = t + SMALL_THREADS * j;
+        if (i < slots) {
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(x[j][e]));
+            const int o = i >= npk * 64 ? 1 : 0;
+            atomicMax(&rmax[o][(i - o * npk * 64) & 31], __float_as_int(m));
+        }
+    }
+    __syncthreads();
+    if (t < 64) {
+        const float m = __int_as_float(rmax[t >> 5][t & 31]);
+        sexp[t >> 5][t & 31] = repro_gemm::scale_exponent(m);  // rows past R: m == 0, exponent 0
+    }
+    __syncthreads();
+
+    // Digits of every slot into the panels: buf[((o S + p) npk + kp) 64 + s].
+#pragma unroll
+    for (int j = 0; j < SMALL_SLOTS; ++j) {
+        const int i = t + SMALL_THREADS * j;
+        if (i < slots) {
+            const int o = i >= npk * 64 ? 1 : 0;
+            const int rem = i - o * npk * 64;
+            const int kp = rem >> 6, s = rem & 63;
+            const RowScale rs = row_scale<S>(sexp[o][s & 31]);
+            int dg[S][16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                int d[S];
+                digits_of<S>(round_fixed(x[j][e], rs), d);
+#pragma unroll
+                for (int p = 0; p < S; ++p) dg[p][e] = d[p];
+            }
+#pragma unroll
+            for (int p = 0; p < S; ++p) {
+                v4i w;
+                w[0] = (int)pack4(dg[p][0], dg[p][1], dg[p][2], dg[p][3]);
+                w[1] = (int)pack4(dg[p][4], dg[p][5], dg[p][6], dg[p][7]);
+                w[2] = (int)pack4(dg[p][8], dg[p][9], dg[p][10], dg[p][11]);
+                w[3] = (int)pack4(dg[p][12], dg[p][13], dg[p][14], dg[p][15]);
+                buf[((o * S + p) * npk + kp) * 64 + s] = w;
+            }
+        }
+    }
+    __syncthreads();
+
+    v16i acc[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[l][e] = 0;
+    for (int kp = wave; kp < npk && wave < 4; kp += 4) {
+        v4i fa[S], fb[S];
+#pragma unroll
+        for (int p = 0; p < S; ++p) {
+            fa[p] = buf[(p * npk + kp) * 64 + lane];
+            fb[p] = buf[((S + p) * npk + kp) * 64 + lane];
+        }
+#pragma unroll
+        for (int p = 0; p < S; ++p)
+#pragma unroll
+            for (int q = 0; q < S; ++q)
+                acc[p + q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[p], fb[q], acc[p + q], 0, 0, 0);
+    }
+    __syncthreads();  // every panel read: the buffer now takes the level sums
+    int* red = reinterpret_cast<int*>(buf);
+    if (wave < 4) {
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) red[((wave * L + l) * 16 + e) * 64 + lane] = acc[l][e];
+    }
+    __syncthreads();
+    // Output slot (e, l): accumulator register e of lane l, i.e. row 8 (e / 4) + 4 (l / 32) + e % 4,
+    // column l % 32 of the tile.
+    const int e0 = -14 * (S - 1);
+    {
+        const int i = t;  // one output per thread
+        const int e = i >> 6, ln = i & 63;
+        const int row = 8 * (e >> 2) + 4 * (ln >> 5) + (e & 3), col = ln & 31;
+        const int gr = r0[0] + row, gc = r0[1] + col;
+        if (gr >= a.R || gc >= b.R) return;
+        int lv[L];
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            int v = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) v += red[((w * L + l) * 16 + e) * 64 + ln];
+            lv[l] = v;
+        }
+        C[(size_t)gr * ldc + gc] = round_levels<L>(lv, sexp[0][row] + sexp[1][col] + e0);
+    }
+#endif
+}
+
 // The definition, as plainly as possible: one thread per output, int64 sum of X * Y over
 // this part's share of k. Always writes an int64 partial.
 __global__ void __launch_bounds__(256)
@@ -511,6 +695,31 @@ void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, c
         case 3: launch_mfma_s<3>(L, qa, qb, ea, eb, C, out, partial, stream); break;
         default: break;
     }
+}
+
+void launch_contract_small(const Layout& L, const float* A, const float* B, float* C,
+                           const GemmAddressing& addr, hipStream_t stream) {
+    const int tiles_m = (L.M + 31) / 32, tiles_n = (L.N + 31) / 32;
+    // 16-byte loads for a row-access operand whose rows (and items) start 16-byte aligned
+    auto vec = [&](const float* p, long long ld, long long stride, bool strided) {
+        return !strided && (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0 &&
+               (L.batch == 1 || stride % 4 == 0) && L.K % 4 == 0;
+    };
+    const SmallOperand a{A, addr.lda, L.M, L.a_strided ? 1 : 0,
+                         vec(A, addr.lda, addr.stride_a, L.a_strided) ? 1 : 0};
+    const SmallOperand b{B, addr.ldb, L.N, L.b_strided ? 1 : 0,
+                         vec(B, addr.ldb, addr.stride_b, L.b_strided) ? 1 : 0};
+    const dim3 grid((unsigned)(tiles_m * tiles_n), 1, (unsigned)L.batch);
+#define RG_SMALL(SS)                                                                            \
+    contract_small<SS><<<grid, SMALL_THREADS, 0, stream>>>(a, b, C, L.K, addr.ldc, addr.stride_a, \
+                                                 addr.stride_b, addr.stride_c, tiles_n)
+    switch (L.S) {
+        case 1: RG_SMALL(1); break;
+        case 2: RG_SMALL(2); break;
+        case 3: RG_SMALL(3); break;
+        default: break;
+    }
+#undef RG_SMALL
 }
 
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,

@@ -599,6 +599,7 @@ PlanExtras conv_extras(bool raw) {
     PlanExtras ex;
     ex.raw = raw;
     ex.gemm_bound = false;
+    ex.one_launch = false;  // the pipeline's options (gathering, group scales) are needed
     return ex;
 }
 

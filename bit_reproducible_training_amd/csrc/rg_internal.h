@@ -43,6 +43,25 @@ __device__ __forceinline__ int round_fixed(float x, const RowScale& rs) {
     return min(max(X, -rs.lim), rs.lim);
 }
 
+// Four bytes (low byte of each argument) packed little-endian with v_perm_b32.
+__device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b1, (uint32_t)b0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)b3, (uint32_t)b2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// The balanced base-128 digits of a fixed-point value X (|X| <= 127 * 128^(S-1)), most
+// significant first: X = sum_p d[p] 128^(S-1-p), |d[0]| <= 127, d[p] in [-64, 63] for p > 0.
+template <int S>
+__device__ __forceinline__ void digits_of(int X, int (&d)[S]) {
+#pragma unroll
+    for (int p = S - 1; p >= 1; --p) {
+        d[p] = (X << 25) >> 25;  // v_bfe_i32: the digit in [-64, 63] congruent to X mod 128
+        X = (X + 64) >> 7;       // == (X - digit) / 128 exactly
+    }
+    d[0] = X;
+}
+
 // Largest |x| over a 64-lane wavefront, in every lane.
 __device__ __forceinline__ float wave_max(float m) {
 #pragma unroll
@@ -59,6 +78,8 @@ constexpr int PANEL_ROWS = 32;
 constexpr int PANEL_K = 32;
 constexpr int PANEL_BYTES = 1024;
 constexpr int STEP_K = 64;  // k consumed per pipeline stage of the contraction
+// Longest K of the one-launch small-shape kernel (its digit panels of both operands sit in LDS).
+constexpr int SMALL_MAX_K = 512;
 
 // Where each region lives inside the caller's workspace, and how the work is split. A batch
 // of `batch` independent GEMMs of one shape stacks its items: item b's digit panels, exponents
@@ -68,7 +89,8 @@ struct Layout {
     int S, M, N, K;
     int batch;          // items (1 for the plain GEMM)
     int Mp, Np, Kp;     // padded sizes: Mp, Np multiples of the block tile, Kp of STEP_K
-    int ti, tj;         // MFMA block tile = (64*ti) x (64*tj); 0 for REFERENCE
+    int ti, tj;         // MFMA block tile = (64*ti) x (64*tj); 0 for REFERENCE and small
+    bool small;         // one launch of contract_small (32x32 tiles, no workspace use)
     int split;          // split-K parts
     bool ta, tb;
     bool a_strided, b_strided;  // operand read along k with a stride (column access)
@@ -96,6 +118,7 @@ struct PlanExtras {
     bool raw = false;
     bool gemm_bound = true;
     int batch = 1;
+    bool one_launch = true;  // the small-shape kernel may be chosen (plain GEMMs only)
 };
 
 // Builds the layout; returns a hipError_t code (0, InvalidValue, NotSupported).
@@ -199,6 +222,9 @@ struct OutAddr {
 void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, const int* ea,
                           const int* eb, float* C, OutAddr out, int64_t* partial,
                           hipStream_t stream);
+// Whole GEMM (or batch) in one launch, for a layout with L.small.
+void launch_contract_small(const Layout& L, const float* A, const float* B, float* C,
+                           const GemmAddressing& addr, hipStream_t stream);
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,
                                int64_t* partial, hipStream_t stream);
 void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,

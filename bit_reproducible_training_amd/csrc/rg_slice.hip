@@ -222,13 +222,6 @@ __global__ void __launch_bounds__(256) absmax_kernel(SliceDesc a, SliceDesc b) {
     }
 }
 
-// Four bytes (low byte of each argument) packed little-endian with v_perm_b32.
-__device__ __forceinline__ uint32_t pack4(int b0, int b1, int b2, int b3) {
-    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b1, (uint32_t)b0, 0x0c0c0400u);
-    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)b3, (uint32_t)b2, 0x0c0c0400u);
-    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-}
-
 // Rounds 16 values and writes them: S digit planes of 16 bytes (balanced base 128, most
 // significant first: X = sum_p d_p 128^(S-1-p), |d_0| <= 127, d_p in [-64, 63] for p > 0),
 // or 16 int32 fixed-point values for INT32_OUT.

@@ -94,7 +94,9 @@ def test_not_supported_off_gfx950():
 def test_auto_resolves_to_mfma():
     p, _ = _plan(4096, 4096, 4096)
     assert p.algo == rg.Algo.TensorCore and (p.tile_m, p.tile_n) == (128, 128)
-    p, _ = _plan(64, 10, 84)
+    p, _ = _plan(64, 10, 84)              # small: the one-launch kernel's 32x32 tiles
+    assert p.algo == rg.Algo.TensorCore and (p.tile_m, p.tile_n) == (32, 32)
+    p, _ = _plan(64, 10, 84, tile_m=64, tile_n=64)
     assert p.algo == rg.Algo.TensorCore and (p.tile_m, p.tile_n) == (64, 64)
     p, _ = _plan(256, 256, 256, algo=rg.Algo.Tiled)
     assert p.algo == rg.Algo.Tiled and (p.tile_m, p.tile_n) == (64, 64)
@@ -148,6 +150,37 @@ def test_default_plan_follows_the_cost_model():
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
 
 
+def test_small_shapes_take_the_one_launch_kernel():
+    """Plain GEMMs with K <= 512 and at most one 32x32 tile per compute unit run as one launch
+    (nothing of the workspace used); a pinned 64/128 tile, Tiled, an explicit split or a longer K
+    keep the pipeline, and a pinned 32x32 tile asks for the one-launch kernel whenever K allows."""
+    for M, N, K in ((256, 256, 256), (64, 120, 400), (64, 400, 120), (120, 400, 64), (64, 10, 84),
+                    (10, 84, 64), (1, 1, 1), (33, 47, 512)):
+        for S in (1, 2, 3):
+            p, info = _plan(M, N, K, slices=S)
+            assert (p.tile_m, p.tile_n, p.split_k) == (32, 32, 1), (M, N, K, S)
+            assert p.algo == rg.Algo.TensorCore and info.part == -1
+            assert 0 < p.workspace_bytes <= 256
+    for kw in (dict(tile_m=64, tile_n=64), dict(algo=rg.Algo.Tiled), dict(split_k=2),
+               dict(algo=rg.Algo.Reference)):
+        p, _ = _plan(64, 120, 400, **kw)
+        assert (p.tile_m, p.tile_n) != (32, 32), kw
+    p, _ = _plan(64, 120, 513)            # K past the kernel's LDS panels
+    assert (p.tile_m, p.tile_n) == (64, 64)
+    p, _ = _plan(512, 512, 512)           # 256 tiles: one per compute unit
+    assert (p.tile_m, p.tile_n) == (32, 32)
+    p, _ = _plan(512, 544, 512)           # 272 tiles
+    assert (p.tile_m, p.tile_n) != (32, 32)
+    p, _ = rg.plan_for_device(512, 544, 512, rg.Config(), is_gfx950=True, num_cus=304)
+    assert (p.tile_m, p.tile_n) == (32, 32)
+    p, _ = _plan(4096, 4096, 256)         # too many tiles: the pipeline
+    assert (p.tile_m, p.tile_n) != (32, 32)
+    p, _ = _plan(4096, 4096, 256, tile_m=32, tile_n=32)   # pinned
+    assert (p.tile_m, p.tile_n) == (32, 32)
+    p, _ = _plan(64, 64, 1024, tile_m=32, tile_n=32)      # pinned, but K too long: planner's choice
+    assert (p.tile_m, p.tile_n) != (32, 32)
+
+
 def test_split_clamped_to_k_steps():
     p, _ = _plan(4096, 4096, 100, split_k=64)
     assert p.split_k == 2  # Kp = 128 -> two stages of 64
@@ -156,7 +189,8 @@ def test_split_clamped_to_k_steps():
 
 
 def test_workspace_layout_regions():
-    for kw in (dict(), dict(split_k=4), dict(algo=rg.Algo.Reference, split_k=3), dict(slices=1)):
+    for kw in (dict(tile_m=64, tile_n=64), dict(split_k=4), dict(algo=rg.Algo.Reference, split_k=3),
+               dict(slices=1, tile_m=128, tile_n=64)):
         p, info = _plan(133, 77, 301, **kw)
         S = kw.get("slices", 3)
         elem = 4 if kw.get("algo") == rg.Algo.Reference else S

@@ -166,7 +166,9 @@ def test_slicing_routes_digits_exponents_and_result(torch_gpu, M, N, K, ta, tb):
     A[:K] = 0.0
     for S in ((1, 2, 3) if K in (1000, 2052, 200) else (3,)):
         X, Y, eA, eB = O.quantize(A, B, M, N, K, ta, tb, S)
-        cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb)
+        # the pipeline's tile pinned: short K would otherwise take the one-launch kernel, which
+        # leaves the workspace unused
+        cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb, tile_m=64, tile_n=64)
         note("slice route M=%d N=%d K=%d ta=%d tb=%d S=%d" % (M, N, K, ta, tb, S))
         C, plan, ws = run(torch, A, B, M, N, K, cfg)
         info = rg.workspace_layout(M, N, K, cfg)
@@ -234,7 +236,7 @@ def test_row_maxima_short_rows(torch_gpu, K):
     want = O.cpu_gemm(A, B, M, N, K, 0, 1, 3).view(np.uint32)
     dA, dB = to_dev(torch, A), to_dev(torch, B)
     for algo in (rg.Algo.Reference, rg.Algo.TensorCore):
-        cfg = rg.Config(algo=algo, trans_b=True)
+        cfg = rg.Config(algo=algo, trans_b=True, tile_m=64, tile_n=64)  # the pipeline's slicing
         note("short rows K=%d algo=%s" % (K, algo.name))
         C, plan, ws = run(torch, dA, dB, M, N, K, cfg)
         info = rg.workspace_layout(M, N, K, cfg)
