@@ -34,9 +34,13 @@ sys.path.insert(0, REPO)
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 # HBM bytes per launch of the contraction at 4096^3 S=3 (fetch + write), from rocprofv3
-# FETCH_SIZE / WRITE_SIZE scaled by the same counters on a 256 MiB device copy; see
-# profiles/contract_mfma_4096cube_traffic.md. Updated when the kernel changes.
-TRAFFIC_BYTES = 671543144
+# FETCH_SIZE / WRITE_SIZE scaled by the same counters on a 256 MiB device copy
+# (profiles/contract_mfma_4096cube_traffic.md), measured on the contraction source whose SHA-256
+# is TRAFFIC_SOURCE_SHA256. A counter value cannot be read from inside this process, so the
+# figure is reported only while that source is unchanged; otherwise traffic is null.
+TRAFFIC_BYTES = 671478502
+TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
+TRAFFIC_SOURCE_SHA256 = "e9e33fcab24dce32d2f1e8f31769e505a1024e7c55d12d6964fb693622bd6da4"
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
@@ -44,6 +48,18 @@ FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 # SplitMix64 in numpy: draw i of seed s is mix(s + (i + 1) * gamma).
 # --------------------------------------------------------------------------------------
 _G = np.uint64(0x9E3779B97F4A7C15)
+
+
+def measured_traffic():
+    """TRAFFIC_BYTES if the contraction source is the one it was measured on, else None."""
+    import hashlib
+
+    try:
+        with open(TRAFFIC_SOURCE, "rb") as f:
+            digest = hashlib.sha256(f.read()).hexdigest()
+    except OSError:
+        return None
+    return TRAFFIC_BYTES if digest == TRAFFIC_SOURCE_SHA256 else None
 
 
 def _draw(seed, idx):
@@ -885,7 +901,10 @@ def main():
                       "final": round(head["final_ms"], 4)},
         "roofline": {"bound": "mfma", "achieved": round(contract_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(contract_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": TRAFFIC_BYTES,
+                     "traffic": measured_traffic(),
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, scaled by a "
+                                       "256 MiB copy (profiles/contract_mfma_4096cube_traffic.md); "
+                                       "null when rg_contract.hip differs from the measured source",
                      "kernel": "contract_mfma<3,2,1,2,4>: int8 ops = 9 * 2MNK per launch, one "
                                "launch per step; achieved = ops / HIP-event duration"},
         # The slicing stage against the HBM roofline: algorithmic bytes = fp32 inputs read once
