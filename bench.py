@@ -608,7 +608,8 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
     """One JSON line: every GEMM of BASELINE configurations 1, 2, 3 and 5 timed on the GPU in
     steady state: back-to-back GEMMs for about `warm_ms` of GPU time (past the GPU's
     power-management transient after a change of load), then HIP events around about `timed_ms`
-    of back-to-back GEMMs (at least 10). Reports effective FP32 TFLOP/s, the stage times (median of
+    of back-to-back GEMMs (at least 10), the GPU brought out of idle first (warm_gpu). Reports
+    effective FP32 TFLOP/s, the stage times (median of
     5 runs with stage events: slicing, contraction, final rounding), the contraction's share of the
     dense int8 MFMA peak, the plan, and whether the runs gave identical bits. GEMMs of less than
     0.1 ms also get `graph_ms`, the GPU time per GEMM without the host's launch cost."""
@@ -616,7 +617,10 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
     gen.manual_seed(2024)
     sp = torch.cuda.current_stream().cuda_stream
     rows = []
+    warm_gpu(torch, rg)
     for name, M, N, K, ta, tb, S, sa, sb in _config_cases():
+        if name == "c3.qkv.fwd":  # after the tiny LeNet GEMMs, which leave the GPU almost idle
+            warm_gpu(torch, rg)
         def draw(n, scale):
             if scale < 0:  # U(-|scale|, |scale|)
                 return (torch.rand(n, device="cuda", generator=gen) * 2 - 1) * -scale
@@ -681,22 +685,47 @@ SWEEP_SHAPES = [("sq4096", 4096, 4096, 4096, 0, 0), ("sq2048", 2048, 2048, 2048,
                 ("r2048x8192x1024", 2048, 8192, 1024, 0, 0)]
 
 
+def warm_gpu(torch, rg, ms=400.0):
+    """About `ms` of back-to-back 4096^3 GEMMs: takes the GPU past the power-management
+    transient that follows idle, so that the first timings are not slowed by it."""
+    n = 4096
+    A = torch.randn(n * n, device="cuda")
+    B = torch.randn(n * n, device="cuda")
+    C = torch.empty(n * n, device="cuda")
+    cfg = rg.Config()
+    plan = rg.make_plan(n, n, n, cfg)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    sp = torch.cuda.current_stream().cuda_stream
+    for _ in range(int(ms / 0.5)):
+        code = rg.repro_gemm_fp32_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), n, n, n, cfg,
+                                     ws.data_ptr(), ws.numel(), sp, None)
+        if code != 0:
+            raise rg.ReproGemmError(code, "warm_gpu")
+    torch.cuda.synchronize()
+    del A, B, C, ws
+    torch.cuda.empty_cache()
+
+
+SWEEP_TILES = ((128, 128), (128, 64), (64, 128), (64, 64), (64, 192), (192, 64))
+
+
 def sweep_plans(torch, rg, warm_ms=15.0, timed_ms=15.0):
-    """One JSON line per shape: every block tile (128x128, 128x64, 64x128, 64x64) x split_k in
-    {1, 2, 3, 4, 6, 8, 12, 16} forced through Config, each timed over about `timed_ms` of
-    back-to-back GEMMs after about `warm_ms` (S = 3), next to the plan the planner picks. The
-    data the planner's cost model (rg_api.cpp::plan_cost) is fitted to."""
+    """One JSON line per shape: every block tile (SWEEP_TILES) x split_k in {1, 2, 3, 4, 6, 8,
+    12, 16} forced through Config, each timed over about `timed_ms` of back-to-back GEMMs after
+    about `warm_ms` (S = 3; the GPU warmed first), next to the plan the planner picks. The data
+    the planner's cost model (rg_api.cpp::plan_cost) is fitted to."""
     cases = [(c[0], c[1], c[2], c[3], c[4], c[5]) for c in _config_cases() if c[0].startswith(("c3", "c5"))]
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2024)
     sp = torch.cuda.current_stream().cuda_stream
+    warm_gpu(torch, rg)
     for name, M, N, K, ta, tb in cases + SWEEP_SHAPES:
         dA = torch.randn(M * K, device="cuda", generator=gen)
         dB = torch.randn(K * N, device="cuda", generator=gen)
         C = torch.empty((M, N), device="cuda")
         auto = rg.make_plan(M, N, K, rg.Config(trans_a=ta, trans_b=tb))
         res, seen = [], set()
-        for tm, tn in ((128, 128), (128, 64), (64, 128), (64, 64)):
+        for tm, tn in SWEEP_TILES:
             for split in (1, 2, 3, 4, 6, 8, 12, 16):
                 cfg = rg.Config(trans_a=ta, trans_b=tb, tile_m=tm, tile_n=tn, split_k=split)
                 plan = rg.make_plan(M, N, K, cfg)

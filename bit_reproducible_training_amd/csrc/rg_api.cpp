@@ -72,10 +72,11 @@ void choose_chunks(int R, int rows, int K, bool strided, int* nch, int* kch) {
 // block slots (compute units x blocks resident per compute unit, from the block's LDS ring);
 // a block costs a fixed prologue/epilogue plus one pipeline stage per 64 values of k of its
 // part; a split adds the int64 partials' traffic (written once, read once) at about 4 TB/s.
-// Constants are fitted to MI355X measurements of every block tile x split on 22 shapes (the
-// GPT-2 and LM-head GEMMs of the BASELINE configurations, squares, tall and long-K shapes; the
-// plan picked is the fastest measured, or within 7% of it) at S = 3, and scaled by the MFMA work
-// per stage, S^2, for fewer slices.
+// The per-tile constants (S = 3) were chosen so that the planner picks the fastest measured plan
+// on a sweep of every block tile x split over 22 shapes on MI355X (the GEMMs of BASELINE
+// configurations 3 and 5, squares, tall and long-K shapes; the GPU brought out of idle first):
+// 20 of the 22 picks are the fastest measured plan, the others within 2.2% and 10.5% of it. The
+// stage time's MFMA part scales with S^2 for fewer slices.
 // Blocks of one MFMA tile resident per compute unit: the LDS ring (3 stages of the block's
 // digit panels) against 160 KiB, at most 2.
 int blocks_per_cu(int ti, int tj, int S) {
@@ -89,9 +90,20 @@ double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split,
     const int per_cu = blocks_per_cu(ti, tj, S);
     const double slots = (double)std::max(1, num_cus) * per_cu;
     const double waves = std::ceil(tiles * split / slots);
-    const double w = ti * tj / 4.0;  // work of a block stage relative to the 128x128 tile
-    const double stage_us = 0.1 + 1.4 * w * per_cu * (S * S / 9.0);
-    const double fixed_us = 1.0 + 4.0 * w * per_cu;
+    // per block wave at S = 3: 128x128 (8 wavefronts, one block per CU), 64x64 (4 wavefronts,
+    // two per CU), 64x192 and 192x64 (12 wavefronts), and the pinned-only 128x64 and 64x128
+    double stage3 = 0.8, fixed_us = 3.0;
+    if (ti == 2 && tj == 2) {
+        stage3 = 1.276;
+        fixed_us = 8.5;
+    } else if (ti == 1 && tj == 1) {
+        stage3 = 0.803;
+        fixed_us = 3.0;
+    } else if (ti * tj == 3) {
+        stage3 = 0.978;
+        fixed_us = 9.66;
+    }
+    const double stage_us = 0.1 + (stage3 - 0.1) * (S * S / 9.0);
     const double steps = std::ceil((double)nsteps / split);
     double t = waves * (steps * stage_us + fixed_us);
     if (split > 1 || raw) {
@@ -99,6 +111,13 @@ double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split,
         t += 3.0 + (8.0 * outs * (split + 1) + 4.0 * outs) / 4.0e6;
     }
     return t;
+}
+
+// Block tiles a caller may pin through Config.tile_m / tile_n: 64 or 128 by 64 or 128, and (at
+// S = 3) the twelve-wavefront 64x192 and 192x64.
+bool pinned_tile(int tile_m, int tile_n, int S) {
+    if ((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128)) return true;
+    return S == 3 && ((tile_m == 64 && tile_n == 192) || (tile_m == 192 && tile_n == 64));
 }
 
 // The one-launch small-shape kernel (contract_small): for plain GEMMs with the default split and
@@ -113,7 +132,7 @@ bool small_path(int M, int N, int K, int batch, int split_k, int tile_m, int til
     if (algo == RG_ALGO_TILED || split_k != 1 || K > SMALL_MAX_K) return false;
     if (!extras.one_launch || extras.raw || !extras.gemm_bound) return false;
     if (tile_m == 32 && tile_n == 32) return true;
-    if ((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128)) return false;
+    if (pinned_tile(tile_m, tile_n, 3)) return false;
     const double tiles = (double)ceil_div(M, 32) * ceil_div(N, 32) * batch;
     return tiles <= std::max(1, num_cus);
 }
@@ -172,15 +191,19 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
         // that minimum, the next 8 splits and the splits that exactly fill 1..16 waves of the
         // GPU's block slots. The planner keeps the candidate with the lowest estimated time
         // (plan_cost); ties keep the earlier candidate.
-        int tiles_cand[2][2];
+        int tiles_cand[4][2];
         int ntile = 0;
         if (algo == RG_ALGO_TILED) {
             tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 1;
-        } else if ((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128)) {
+        } else if (pinned_tile(tile_m, tile_n, S)) {
             tiles_cand[ntile][0] = tile_m / 64; tiles_cand[ntile++][1] = tile_n / 64;
         } else {
             tiles_cand[ntile][0] = 2; tiles_cand[ntile++][1] = 2;
             tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 1;
+            if (S == 3) {
+                tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 3;
+                tiles_cand[ntile][0] = 3; tiles_cand[ntile++][1] = 1;
+            }
         }
         const int split_lo = std::min(std::max(split_k, min_split), nsteps);
         double best = -1.0;

@@ -87,13 +87,16 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 #define RG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // Wavefronts per SIMD that the block tile's LDS ring allows (blocks per CU x wavefronts per
-// block / 4), capped at 2: the register budget the kernel is compiled for (at most 512 / that).
+// block / 4), capped at 2 unless one block alone needs more (12 wavefronts: 3): the register
+// budget the kernel is compiled for (at most 512 / that).
 template <int S, int WTI, int WTJ, int WGM, int WGN>
 constexpr int contract_waves_per_simd() {
     constexpr int lds = 3 * (WGM * WTI + WGN * WTJ) * 2 * S * PANEL_BYTES;
     constexpr int blocks = (160 * 1024) / lds;
+    constexpr int need = (WGM * WGN + 3) / 4;  // one block's wavefronts per SIMD
     constexpr int w = blocks * WGM * WGN / 4;
-    return w < 1 ? 1 : (w > 2 ? 2 : w);
+    constexpr int cap = need > 2 ? need : 2;
+    return w < need ? need : (w > cap ? cap : w);
 }
 
 template <int S, int WTI, int WTJ, int WGM, int WGN>
@@ -672,9 +675,22 @@ static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, c
                           hipStream_t stream) {
     const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)L.split, (unsigned)L.batch);
-    // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64, 64x128, 64x64 = 4 wavefronts.
+    // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64, 64x128, 64x64 = 4 wavefronts;
+    // 64x192 and 192x64 = 12 wavefronts of 32x32 (three per SIMD).
 #define RG_CONTRACT_ARGS qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n, L.Mp, L.Np, \
                          out.ldc, out.c_item
+    // (The twelve-wavefront tiles exist for S = 3 only: their 48 stage panels split evenly over
+    // 12 wavefronts; the planner never gives them to S < 3.)
+    if constexpr (S == 3) {
+        if (L.ti == 1 && L.tj == 3) {
+            contract_mfma<S, 1, 1, 2, 6><<<grid, 768, 0, stream>>>(RG_CONTRACT_ARGS);
+            return;
+        }
+        if (L.ti == 3 && L.tj == 1) {
+            contract_mfma<S, 1, 1, 6, 2><<<grid, 768, 0, stream>>>(RG_CONTRACT_ARGS);
+            return;
+        }
+    }
     if (L.ti == 2 && L.tj == 2)
         contract_mfma<S, 2, 1, 2, 4><<<grid, 512, 0, stream>>>(RG_CONTRACT_ARGS);
     else if (L.ti == 2 && L.tj == 1)

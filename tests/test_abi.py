@@ -102,11 +102,14 @@ def test_auto_resolves_to_mfma():
     assert p.algo == rg.Algo.Tiled and (p.tile_m, p.tile_n) == (64, 64)
 
 
-@pytest.mark.parametrize("tm,tn", [(128, 128), (128, 64), (64, 128), (64, 64)])
+@pytest.mark.parametrize("tm,tn", [(128, 128), (128, 64), (64, 128), (64, 64), (64, 192), (192, 64)])
 def test_tile_hints(tm, tn):
     p, info = _plan(300, 200, 100, tile_m=tm, tile_n=tn)
     assert (p.tile_m, p.tile_n) == (tm, tn)
     assert info.Mp % tm == 0 and info.Np % tn == 0 and info.Mp >= 300 and info.Np >= 200
+    if tm == 192 or tn == 192:  # twelve-wavefront tiles: S = 3 only, else the planner's choice
+        p, _ = _plan(300, 200, 100, tile_m=tm, tile_n=tn, slices=2)
+        assert (p.tile_m, p.tile_n) != (tm, tn)
 
 
 @pytest.mark.parametrize("S,limit", [(1, 133120), (2, 132096), (3, 105472)])
@@ -122,32 +125,42 @@ def test_split_raised_for_exact_int32(S, limit):
 
 
 def test_default_plan_follows_the_cost_model():
-    """With the default split_k = 1 and tile hints, the planner picks the block tile and split
-    with the lowest estimated time: waves of blocks over the GPU's block slots times the
-    stages of a part, plus the int64 partials of a split. The cases below were measured on
-    MI355X over every block tile x split, and the chosen plan was the fastest or within 7% of it
-    (qkv.dW, attn_proj.dW and 512x512x8192 are the 6-7% ones). An explicit split_k is
-    honoured; one-stage K is never split."""
+    """With the default split_k = 1 and tile hints, the planner picks the block tile (128x128,
+    64x64, and at S = 3 the twelve-wavefront 64x192 / 192x64) and split with the lowest
+    estimated time: waves of blocks over the GPU's block slots times the stages of a part, plus
+    the int64 partials of a split. The cases below were measured on MI355X over every block tile
+    x split, and the chosen plan was the fastest (512x512x8192 within 10.5%). An explicit split_k
+    is honoured; one-stage K is never split."""
     p, _ = _plan(64, 64, 65536)           # 1 tile, 1024 stages: one wave of 512 parts
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 512)
     p, _ = _plan(1024, 64, 1024)          # 16 tiles of 64x64, 16 stages: split to fill a wave
     assert (p.tile_m, p.tile_n) == (64, 64) and p.split_k >= 8
-    p, _ = _plan(3072, 768, 8192, trans_a=True)   # 144 tiles of 128x128: split 3 = 432 blocks
-    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 3)
+    p, _ = _plan(3072, 768, 8192, trans_a=True)   # 192 tiles of 64x192 = one wave, no partials
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 1)
+    p, _ = _plan(768, 768, 8192, trans_a=True)    # 48 tiles of 64x192 x 5 parts
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 5)
+    p, _ = _plan(2304, 768, 8192, trans_a=True)   # 108 tiles of 128x128 x 2 parts
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 2)
+    p, _ = _plan(8192, 768, 3072)         # 512 tiles of 64x192 = two waves of 48 stages
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 1)
     p, _ = _plan(1024, 1024, 65536)       # 64 tiles of 128x128, 1024 stages
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 4)
     p, _ = _plan(8192, 768, 768, trans_b=True)    # 1536 tiles of 64x64 = 3 waves of 512
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 1)
     p, _ = _plan(1024, 768, 768, trans_b=True)    # one wave either way: no split traffic
     assert p.split_k == 1
-    p, _ = _plan(8192, 2304, 768, trans_b=True)   # 4.5 waves of 128x128 vs 9 of 64x64: measured
-    assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 1)     # 0.148 vs 0.132 ms, 64x64 wins
+    p, _ = _plan(8192, 2304, 768, trans_b=True)   # 12 stages: 64x64's short prologue wins
+    assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 1)
+    p, _ = _plan(50257, 768, 8192, trans_a=True)  # LM-head weight gradient
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
     p, _ = _plan(1024, 1024, 64)          # one stage only
     assert p.split_k == 1
     p, _ = _plan(1024, 64, 1024, split_k=2)
     assert p.split_k == 2
     p, _ = _plan(4096, 4096, 4096)        # 1024 tiles of 128x128 = 4 full waves
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
+    p, _ = _plan(8192, 768, 3072, slices=2)   # the twelve-wavefront tiles exist at S = 3 only
+    assert (p.tile_m, p.tile_n) in ((128, 128), (64, 64))
 
 
 def test_small_shapes_take_the_one_launch_kernel():

@@ -17,7 +17,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 SPLITS = (1, 2, 3, 7, 16, 64)
-TILES = ((128, 128), (128, 64), (64, 128), (64, 64))
+TILES = ((128, 128), (128, 64), (64, 128), (64, 64), (64, 192), (192, 64))
 MAX_WS_BYTES = 24 << 30
 
 

@@ -73,13 +73,36 @@ def test_tile_and_split_invariance(torch_gpu):
     want = O.cpu_gemm(A, B, M, N, K, 0, 1, 3).view(np.uint32)
     dA, dB = to_dev(torch, A), to_dev(torch, B)
     ws = None
-    for tm, tn in ((128, 128), (128, 64), (64, 128), (64, 64)):
+    for tm, tn in ((128, 128), (128, 64), (64, 128), (64, 64), (64, 192), (192, 64)):
         for split in (1, 2, 5, 16, 33):
             note("tiles %dx%d split %d" % (tm, tn, split))
             cfg = rg.Config(tile_m=tm, tile_n=tn, split_k=split, trans_b=True)
             C, plan, ws = run(torch, dA, dB, M, N, K, cfg, ws=ws)
             assert (plan.tile_m, plan.tile_n) == (tm, tn)
             assert np.array_equal(bits(C), want), (tm, tn, split)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_twelve_wave_tiles_ragged(torch_gpu, ta, tb):
+    """The 64x192 and 192x64 tiles (S = 3) on shapes that are no multiple of 192 in either
+    direction, with the stress values of the hash tool, every transpose and several splits."""
+    from test_oracle import _stress_inputs
+
+    torch = torch_gpu
+    rng = np.random.default_rng(50 + 2 * ta + tb)
+    for M, N, K in ((200, 391, 777), (450, 70, 1290), (64, 192, 64)):
+        A, B = _stress_inputs(M, N, K, rng)
+        want = O.cpu_gemm(A.ravel(), B.ravel(), M, N, K, 0, 0, 3).view(np.uint32)
+        As = np.ascontiguousarray(A.T) if ta else A
+        Bs = np.ascontiguousarray(B.T) if tb else B
+        dA, dB = to_dev(torch, As), to_dev(torch, Bs)
+        for tm, tn in ((64, 192), (192, 64)):
+            for split in (1, 3, 7):
+                note("12-wave tiles %dx%d M=%d N=%d K=%d ta=%d tb=%d split=%d" % (tm, tn, M, N, K, ta, tb, split))
+                cfg = rg.Config(tile_m=tm, tile_n=tn, split_k=split, trans_a=bool(ta), trans_b=bool(tb))
+                C, plan, _ = run(torch, dA, dB, M, N, K, cfg)
+                assert (plan.tile_m, plan.tile_n) == (tm, tn)
+                assert np.array_equal(bits(C), want), (M, N, K, tm, tn, split)
 
 
 def _suite():
