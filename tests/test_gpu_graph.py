@@ -33,16 +33,24 @@ def _capture(torch, fn):
     return g
 
 
-@pytest.mark.parametrize("M,N,K,ta,tb,split", [(384, 320, 1000, 0, 0, 1), (200, 130, 5000, 1, 0, 3),
-                                               (256, 64, 4096, 0, 1, 1), (1024, 1024, 64, 0, 1, 1)])
-def test_gemm_replays_equal_eager(torch_gpu, M, N, K, ta, tb, split):
+@pytest.mark.parametrize("M,N,K,ta,tb,split,tile", [
+    (384, 320, 1000, 0, 0, 1, 16), (200, 130, 5000, 1, 0, 3, 16), (256, 64, 4096, 0, 1, 1, 16),
+    (1024, 1024, 64, 0, 1, 1, 16),
+    (256, 256, 256, 0, 0, 1, 16), (64, 120, 400, 0, 1, 1, 16),    # one-launch small kernel
+    (300, 500, 1500, 1, 0, 1, (64, 192)), (500, 300, 700, 0, 1, 2, (192, 64))])  # 12 wavefronts
+def test_gemm_replays_equal_eager(torch_gpu, M, N, K, ta, tb, split, tile):
     torch = torch_gpu
     torch.manual_seed(M + N + K)
     A = torch.randn(M * K, device="cuda")
     B = torch.randn(K * N, device="cuda")
     C = torch.empty(M, N, device="cuda")
-    cfg = rg.Config(trans_a=ta, trans_b=tb, split_k=split)
+    tm, tn = tile if isinstance(tile, tuple) else (tile, tile)
+    cfg = rg.Config(trans_a=ta, trans_b=tb, split_k=split, tile_m=tm, tile_n=tn)
     plan = rg.make_plan(M, N, K, cfg)
+    if M * N <= 256 * 256 and K <= 512 and tile == 16:
+        assert (plan.tile_m, plan.tile_n) == (32, 32)
+    if isinstance(tile, tuple):
+        assert (plan.tile_m, plan.tile_n) == tile
     ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
 
     def call():
