@@ -658,6 +658,16 @@ static long long onepass_blocks(const SliceDesc& d) {
     return (strips + 31) / 32 * 32;
 }
 
+// k panels per wavefront of the block-strip one pass: the smallest instantiated count with which
+// the 8 wavefronts cover every k panel, so few wavefronts of a block sit idle (K = 768: 3 each;
+// K = 2304: 9).
+static int onepass_nf4(int Kp) {
+    const int need = (Kp / PANEL_K + 7) / 8;
+    for (int nf : {3, 4, 6, 8, 9, 12, 16})
+        if (nf >= need) return nf;
+    return 16;
+}
+
 bool onepass_eligible(const SliceDesc& d) {
     return d.Kp <= (d.strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K);
 }
@@ -696,42 +706,48 @@ void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use
     const long long nb = use_b ? onepass_blocks(b) : 0;
     if (na + nb == 0) return;
     const unsigned blocks = (unsigned)(na + nb);
-    const int nf4 = kp <= 1024 ? 4 : (kp <= 2048 ? 8 : 16);
+    const int nf4 = onepass_nf4(kp);
 #define RG_ONEPASS(SS, NF)                                                                      \
     (gather ? slice_onepass_kernel<SS, NF, false, true><<<blocks, 512, 0, stream>>>(a, b, na)    \
             : slice_onepass_kernel<SS, NF, false, false><<<blocks, 512, 0, stream>>>(a, b, na))
+#define RG_ONEPASS_S(SS)                                                                        \
+    case SS * 100 + 3: RG_ONEPASS(SS, 3); break;                                                \
+    case SS * 100 + 4: RG_ONEPASS(SS, 4); break;                                                \
+    case SS * 100 + 6: RG_ONEPASS(SS, 6); break;                                                \
+    case SS * 100 + 8: RG_ONEPASS(SS, 8); break;                                                \
+    case SS * 100 + 9: RG_ONEPASS(SS, 9); break;                                                \
+    case SS * 100 + 12: RG_ONEPASS(SS, 12); break;                                              \
+    case SS * 100 + 16: RG_ONEPASS(SS, 16); break;
     switch (S * 100 + nf4) {
-        case 104: RG_ONEPASS(1, 4); break;
-        case 108: RG_ONEPASS(1, 8); break;
-        case 116: RG_ONEPASS(1, 16); break;
-        case 204: RG_ONEPASS(2, 4); break;
-        case 208: RG_ONEPASS(2, 8); break;
-        case 216: RG_ONEPASS(2, 16); break;
-        case 304: RG_ONEPASS(3, 4); break;
-        case 308: RG_ONEPASS(3, 8); break;
-        case 316: RG_ONEPASS(3, 16); break;
+        RG_ONEPASS_S(1)
+        RG_ONEPASS_S(2)
+        RG_ONEPASS_S(3)
         default: break;
     }
+#undef RG_ONEPASS_S
 #undef RG_ONEPASS
 }
 
 void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream) {
     const long long n1 = onepass_blocks(one);
     const unsigned blocks = (unsigned)(n1 + absmax8_blocks(two));
-    const int nf4 = one.Kp <= 1024 ? 4 : (one.Kp <= 2048 ? 8 : 16);
+    const int nf4 = onepass_nf4(one.Kp);
 #define RG_FUSED(SS, NF) onepass_absmax_kernel<SS, NF><<<blocks, 512, 0, stream>>>(one, two, n1)
+#define RG_FUSED_S(SS)                                                                          \
+    case SS * 100 + 3: RG_FUSED(SS, 3); break;                                                  \
+    case SS * 100 + 4: RG_FUSED(SS, 4); break;                                                  \
+    case SS * 100 + 6: RG_FUSED(SS, 6); break;                                                  \
+    case SS * 100 + 8: RG_FUSED(SS, 8); break;                                                  \
+    case SS * 100 + 9: RG_FUSED(SS, 9); break;                                                  \
+    case SS * 100 + 12: RG_FUSED(SS, 12); break;                                                \
+    case SS * 100 + 16: RG_FUSED(SS, 16); break;
     switch (S * 100 + nf4) {
-        case 104: RG_FUSED(1, 4); break;
-        case 108: RG_FUSED(1, 8); break;
-        case 116: RG_FUSED(1, 16); break;
-        case 204: RG_FUSED(2, 4); break;
-        case 208: RG_FUSED(2, 8); break;
-        case 216: RG_FUSED(2, 16); break;
-        case 304: RG_FUSED(3, 4); break;
-        case 308: RG_FUSED(3, 8); break;
-        case 316: RG_FUSED(3, 16); break;
+        RG_FUSED_S(1)
+        RG_FUSED_S(2)
+        RG_FUSED_S(3)
         default: break;
     }
+#undef RG_FUSED_S
 #undef RG_FUSED
 }
 
