@@ -38,9 +38,9 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 # (profiles/contract_mfma_4096cube_traffic.md), measured on the contraction source whose SHA-256
 # is TRAFFIC_SOURCE_SHA256. A counter value cannot be read from inside this process, so the
 # figure is reported only while that source is unchanged; otherwise traffic is null.
-TRAFFIC_BYTES = 671478502
+TRAFFIC_BYTES = 671469875
 TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
-TRAFFIC_SOURCE_SHA256 = "e9e33fcab24dce32d2f1e8f31769e505a1024e7c55d12d6964fb693622bd6da4"
+TRAFFIC_SOURCE_SHA256 = "e61b99c42d4196da1d69f70e60abaf613899f013bc4eef18939c59c02fcda2fb"
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
