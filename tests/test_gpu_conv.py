@@ -286,3 +286,36 @@ def test_conv_training_steps_are_bitwise_repeatable(torch_gpu):
     first = _lenet_like(torch_gpu)
     note("lenet-like run 2")
     assert _lenet_like(torch_gpu) == first
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_conv_equals_gpu_gemm_on_im2col(torch_gpu, S):
+    """The reference's consumer cross-check (test_repro_conv.cu:84-112) on the GPU: the
+    convolution's forward pass equals the GEMM of the im2col matrix with the filters (W^T), and
+    its weight gradient the GEMM of dY^T with the im2col matrix, bit for bit, both computed on
+    the GPU (whichever algorithm each entry point picks)."""
+    from test_conv import im2col
+
+    torch = torch_gpu
+    for shape in SHAPES + [(16, 3, 32, 32, 8, 3, 3, 1, 1, 1, 1), (100, 6, 14, 14, 16, 5, 5, 1, 1, 0, 0)]:
+        rng = np.random.default_rng(sum(shape) * 5 + S)
+        N, C, H, W, F, KH, KW = shape[:7]
+        OH, OW = O.conv_out_hw(shape)
+        x = rng.standard_normal(N * C * H * W).astype(np.float32)
+        w = (rng.standard_normal(F * C * KH * KW) * 0.1).astype(np.float32)
+        dy = (rng.standard_normal(N * F * OH * OW) * 1e-3).astype(np.float32)
+        cols = im2col(x, shape)
+        Wn, K = cols.shape
+        note("conv vs gemm", shape, "S=%d" % S)
+        y = _run(torch, "fwd", x, w, shape, S)
+        g = rg.gemm(to_dev(torch, cols).reshape(Wn, K), to_dev(torch, w).reshape(F, K), Wn, F, K,
+                    False, True, S)
+        torch.cuda.synchronize()
+        want = np.ascontiguousarray(g.cpu().numpy().reshape(N, OH, OW, F).transpose(0, 3, 1, 2))
+        assert np.array_equal(y.view(np.uint32).ravel(), want.view(np.uint32).ravel()), shape
+        dw = _run(torch, "dW", dy, x, shape, S)
+        D = np.ascontiguousarray(dy.reshape(N, F, OH * OW).transpose(0, 2, 1).reshape(Wn, F))
+        g = rg.gemm(to_dev(torch, D).reshape(Wn, F), to_dev(torch, cols).reshape(Wn, K), F, K, Wn,
+                    True, False, S)
+        torch.cuda.synchronize()
+        assert np.array_equal(dw.view(np.uint32).ravel(), g.cpu().numpy().view(np.uint32).ravel()), shape
