@@ -319,3 +319,47 @@ def test_conv_equals_gpu_gemm_on_im2col(torch_gpu, S):
                     True, False, S)
         torch.cuda.synchronize()
         assert np.array_equal(dw.view(np.uint32).ravel(), g.cpu().numpy().view(np.uint32).ravel()), shape
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_lenet_step_cpu_and_gpu_give_identical_bits(torch_gpu, S):
+    """A LeNet-5-shaped network of the reproducible layers (two Conv2d, three Linear; the
+    pooling done by stride-2 convolutions so that every reduction is one of the library's), one
+    forward and backward pass with a fixed output gradient, on CPU tensors (the CPU half) and on
+    GPU tensors (the MI355X kernels): the output, the input gradient and every parameter
+    gradient are identical bit for bit. ReLU is exact on both devices."""
+    torch = torch_gpu
+    torch.manual_seed(40 + S)
+
+    def lenet():
+        return torch.nn.Sequential(
+            rg.Conv2d(1, 6, 5, padding=2), torch.nn.ReLU(),
+            rg.Conv2d(6, 6, 2, stride=2), torch.nn.ReLU(),
+            rg.Conv2d(6, 16, 5), torch.nn.ReLU(),
+            rg.Conv2d(16, 16, 2, stride=2), torch.nn.ReLU(),
+            torch.nn.Flatten(),
+            rg.Linear(16 * 5 * 5, 120), torch.nn.ReLU(),
+            rg.Linear(120, 84), torch.nn.ReLU(),
+            rg.Linear(84, 10))
+
+    cpu = lenet()
+    gpu = lenet().cuda()
+    gpu.load_state_dict(cpu.state_dict())
+    x = torch.randn(64, 1, 28, 28)
+    dy = torch.randn(64, 10)
+    rg.set_slices(S)
+    try:
+        xc = x.clone().requires_grad_(True)
+        yc = cpu(xc)
+        yc.backward(dy)
+        note("lenet cpu vs gpu S=%d" % S)
+        xg = x.cuda().requires_grad_(True)
+        yg = gpu(xg)
+        yg.backward(dy.cuda())
+        torch.cuda.synchronize()
+    finally:
+        rg.set_slices(3)
+    pairs = [(yc, yg), (xc.grad, xg.grad)]
+    pairs += [(a.grad, b.grad) for a, b in zip(cpu.parameters(), gpu.parameters())]
+    for i, (a, b) in enumerate(pairs):
+        assert torch.equal(a.detach().view(torch.int32), b.detach().cpu().view(torch.int32)), i
