@@ -32,10 +32,10 @@ double max_fixed_point(int S) {
     return top + low;
 }
 
-// Largest |sum over one k of the digit products that share a level|, for balanced
-// base-128 digits (|d0| <= 127, |dp| <= 64 for p > 0):
-//   S=1: 127*127; S=2: level 1 = 2*127*64; S=3: level 2 = 127*64 + 64*64 + 64*127.
-int level_bound_per_k(int S) { return S == 1 ? 16129 : (S == 2 ? 16256 : 20352); }
+// Largest |sum over one k of the digit products that share a level|, for the digits the
+// slicing writes (|d0| <= 127, lower digits in [0, 127]; every product at most 127*127 = 16129
+// in magnitude): S=1: one product; S=2: level 1 has two; S=3: level 2 has three.
+int level_bound_per_k(int S) { return S == 1 ? 16129 : (S == 2 ? 32258 : 48387); }
 
 // Stages (of STEP_K values of k) one part may span with every int32 level sum exact.
 int max_steps_per_part(int S) {

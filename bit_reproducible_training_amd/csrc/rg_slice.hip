@@ -222,9 +222,9 @@ __global__ void __launch_bounds__(256) absmax_kernel(SliceDesc a, SliceDesc b) {
     }
 }
 
-// Rounds 16 values and writes them: S digit planes of 16 bytes (balanced base 128, most
-// significant first: X = sum_p d_p 128^(S-1-p), |d_0| <= 127, d_p in [-64, 63] for p > 0),
-// or 16 int32 fixed-point values for INT32_OUT.
+// Rounds 16 values and writes them: S digit planes of 16 bytes (base 128, most significant
+// first, digits_of: X = sum_p d_p 128^(S-1-p), |d_0| <= 127, d_p in [0, 127] for p > 0), or
+// 16 int32 fixed-point values for INT32_OUT.
 template <int S, bool INT32_OUT>
 __device__ __forceinline__ void emit_panel(const SliceDesc& d, const float (&x)[16], const RowScale& rs,
                                            int rp, int kp, int q, int h, int lane) {
@@ -240,13 +240,10 @@ __device__ __forceinline__ void emit_panel(const SliceDesc& d, const float (&x)[
     int dg[S][16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        int v = X[j];
+        int d[S];
+        digits_of<S>(X[j], d);
 #pragma unroll
-        for (int p = S - 1; p >= 1; --p) {
-            dg[p][j] = (v << 25) >> 25;  // v_bfe_i32: the digit in [-64, 63] congruent to v mod 128
-            v = (v + 64) >> 7;           // == (v - digit) / 128 exactly
-        }
-        dg[0][j] = v;
+        for (int p = 0; p < S; ++p) dg[p][j] = d[p];
     }
     const int npk = d.Kp / PANEL_K;
     uint4* o = reinterpret_cast<uint4*>(d.out) + ((size_t)rp * npk + kp) * S * (PANEL_BYTES / 16) + lane;
@@ -612,13 +609,10 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
         int dg[S][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            int X = round_fixed(x[j], rs);
+            int d[S];
+            digits_of<S>(round_fixed(x[j], rs), d);
 #pragma unroll
-            for (int p = S - 1; p >= 1; --p) {
-                dg[p][j] = (X << 25) >> 25;  // balanced digit in [-64, 63]
-                X = (X + 64) >> 7;
-            }
-            dg[0][j] = X;
+            for (int p = 0; p < S; ++p) dg[p][j] = d[p];
         }
         uint32_t* o = o0 + (size_t)kp * S * (PANEL_BYTES / 4);
 #pragma unroll

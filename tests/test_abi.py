@@ -112,7 +112,7 @@ def test_tile_hints(tm, tn):
         assert (p.tile_m, p.tile_n) != (tm, tn)
 
 
-@pytest.mark.parametrize("S,limit", [(1, 133120), (2, 132096), (3, 105472)])
+@pytest.mark.parametrize("S,limit", [(1, 133120), (2, 66560), (3, 44352)])
 def test_split_raised_for_exact_int32(S, limit):
     """Each part spans at most floor((2^31-1) / level_bound / 64) * 64 values of k."""
     big = 4096  # enough output tiles to occupy 256 compute units: no occupancy split

@@ -160,7 +160,7 @@ def test_slicing_kernel_digits_and_exponents(torch_gpu, S, ta, tb):
         d, Xg = decode_digits(w, off, R, info.Kp, S)
         assert np.abs(d[0]).max() <= 127
         if S > 1:
-            assert d[1:].min() >= -64 and d[1:].max() <= 63
+            assert d[1:].min() >= 0  # lower digits are the bit fields of X
         assert np.array_equal(Xg[:Xo.shape[0], :K], Xo)
         assert not Xg[Xo.shape[0]:].any() and not Xg[:, K:].any()
         e = w[eoff:eoff + 4 * R].view(np.int32)
@@ -200,7 +200,7 @@ def test_slicing_routes_digits_exponents_and_result(torch_gpu, M, N, K, ta, tb):
             d, Xg = decode_digits(w, off, R, info.Kp, S)
             assert np.abs(d[0]).max() <= 127
             if S > 1:
-                assert d[1:].min() >= -64 and d[1:].max() <= 63
+                assert d[1:].min() >= 0  # lower digits are the bit fields of X
             assert np.array_equal(Xg[:Xo.shape[0], :K], Xo)
             assert not Xg[Xo.shape[0]:].any() and not Xg[:, K:].any()
             e = w[eoff:eoff + 4 * R].view(np.int32)
