@@ -174,7 +174,10 @@ def test_slicing_kernel_digits_and_exponents(torch_gpu, S, ta, tb):
 # row or column maxima for the other); and two passes.
 SLICE_ROUTES = [(96, 68, 1000), (100, 64, 2052), (64, 100, 3076), (68, 96, 4100),
                 (96, 64, 1001), (97, 70, 1536), (128, 64, 4096), (96, 68, 200), (97, 70, 61),
-                (64, 100, 128), (33, 9, 25)]
+                (64, 100, 128), (33, 9, 25),
+                # long K, up to the padded K of the reference's tall-skinny case (two passes
+                # with several maxima chunks per row), and a K that is no multiple of 4
+                (40, 36, 9000), (33, 20, 17000), (9, 40, 40000), (24, 8, 65536), (20, 12, 9001)]
 
 
 @pytest.mark.parametrize("M,N,K", SLICE_ROUTES)
