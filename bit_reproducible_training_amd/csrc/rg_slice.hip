@@ -121,9 +121,23 @@ __device__ void absmax_cols(const SliceDesc& d, long long blk) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int cols = d.vec ? 256 : 64;
     const long long groups = (d.R + cols - 1) / cols;
-    if (blk >= (long long)d.batch * groups * d.nch) return;
-    const long long gi = blk / d.nch;
-    const int c = (int)(blk - gi * d.nch);
+    long long gi;
+    int c;
+    if (!d.vec && d.R > 32) {
+        // Unaligned rows: a group's 256-byte run of a k-row shares its end lines with the
+        // neighbouring groups. Block blk runs on XCD blk % 8 (max_blocks is a multiple of 8
+        // here); each XCD takes a contiguous range of (chunk, group) in group order, so
+        // neighbouring groups of one chunk run together on one XCD and fetch those lines once.
+        const long long lin = (blk & 7) * (d.max_blocks / 8) + (blk >> 3);
+        const long long ng = (long long)d.batch * groups;
+        if (lin >= ng * d.nch) return;
+        c = (int)(lin / ng);
+        gi = lin - (long long)c * ng;
+    } else {
+        if (blk >= (long long)d.batch * groups * d.nch) return;
+        gi = blk / d.nch;
+        c = (int)(blk - gi * d.nch);
+    }
     const int b = (int)(gi / groups), g = (int)(gi - (long long)b * groups);
     const float* item = d.src + (size_t)b * d.bstride;
     const int k0 = c * d.kch;
@@ -338,7 +352,18 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
     // Column access: neighbouring blocks take neighbouring row panels of the same k rows;
     // row access: neighbouring blocks continue along k of the same rows.
     int rp, kg;
-    if (d.strided) {
+    if (d.strided && !d.vec) {
+        // Unaligned rows: a panel's 128-byte run of a k-row straddles two lines, each shared
+        // with a neighbouring row panel. Block blk runs on XCD blk % 8 (the dispatcher's round
+        // robin; split_blocks is a multiple of 8 here). Each XCD takes a contiguous range of
+        // (k group, row panel) in panel order, so neighbouring panels run together on one XCD
+        // and fetch the shared lines into its L2 once.
+        const long long per_xcd = d.split_blocks / 8;
+        const long long lin = (blk & 7) * per_xcd + (blk >> 3);
+        if (lin >= (long long)rpanels * kgroups) return;  // padding block (whole block)
+        rp = (int)(lin % rpanels);
+        kg = (int)(lin / rpanels);
+    } else if (d.strided) {
         rp = (int)(blk % rpanels);
         kg = (int)(blk / rpanels);
     } else {
@@ -750,6 +775,7 @@ void slice_grid(SliceDesc& d) {
     if (d.strided) {
         const int cols = d.vec ? 256 : 64;
         d.max_blocks = (long long)d.batch * ((d.R + cols - 1) / cols) * d.nch;
+        if (!d.vec && d.R > 32) d.max_blocks = (d.max_blocks + 7) / 8 * 8;  // whole XCD rounds
     } else {
         const long long per_block = 4LL * rows_per_wave(d);
         d.max_blocks = ((long long)d.batch * d.R * d.nch + per_block - 1) / per_block;
@@ -757,6 +783,7 @@ void slice_grid(SliceDesc& d) {
     const int npk = d.Kp / PANEL_K;
     d.split_blocks = (long long)d.batch * (d.Rp / PANEL_ROWS) *
                      ((npk + 4 * SPLIT_G - 1) / (4 * SPLIT_G));
+    if (d.strided && !d.vec) d.split_blocks = (d.split_blocks + 7) / 8 * 8;  // whole XCD rounds
 }
 
 // Group scales: every row of each group of `group` consecutive rows gets the group's largest

@@ -177,7 +177,10 @@ SLICE_ROUTES = [(96, 68, 1000), (100, 64, 2052), (64, 100, 3076), (68, 96, 4100)
                 (64, 100, 128), (33, 9, 25),
                 # long K, up to the padded K of the reference's tall-skinny case (two passes
                 # with several maxima chunks per row), and a K that is no multiple of 4
-                (40, 36, 9000), (33, 20, 17000), (9, 40, 40000), (24, 8, 65536), (20, 12, 9001)]
+                (40, 36, 9000), (33, 20, 17000), (9, 40, 40000), (24, 8, 65536), (20, 12, 9001),
+                # column access over rows that are not 16-byte aligned (R % 4 != 0), more than 32
+                # columns, padded K past the one-pass limits (XCD-paired maxima and split blocks)
+                (45, 70, 3500), (301, 203, 5001)]
 
 
 @pytest.mark.parametrize("M,N,K", SLICE_ROUTES)
