@@ -37,7 +37,8 @@ def _oracle_item(a, b, ta, tb, S):
 def test_batched_items_equal_single_gemms(torch_gpu, S, ta, tb):
     torch = torch_gpu
     rng = np.random.default_rng(10 * S + 2 * ta + tb)
-    for batch, M, N, K in [(3, 37, 45, 70), (5, 128, 64, 256), (2, 200, 130, 1000), (3, 20, 12, 9000)]:
+    for batch, M, N, K in [(3, 37, 45, 70), (5, 128, 64, 256), (2, 200, 130, 1000), (3, 20, 12, 9000),
+                           (2, 45, 70, 3500)]:
         a_shape = (batch, K, M) if ta else (batch, M, K)
         b_shape = (batch, N, K) if tb else (batch, K, N)
         # Items with very different magnitudes: scales are per item, per row and column.
