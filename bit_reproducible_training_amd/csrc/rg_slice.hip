@@ -99,8 +99,20 @@ __device__ void absmax_rows(const SliceDesc& d, long long blk) {
             m3 = fmaxf(m3, max4(p[q + 192]));
         }
         for (; q < q1; q += 64) m0 = fmaxf(m0, max4(p[q]));
-    } else {
-        for (k = k0 + lane; k + 192 < k1; k += 256) {
+    } else {  // unaligned rows: 16 scalar loads in flight per lane (4 KiB per wavefront)
+        for (k = k0 + lane; k + 960 < k1; k += 1024) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = fabsf(row[k + 64 * j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                m0 = fmaxf(m0, v[4 * j]);
+                m1 = fmaxf(m1, v[4 * j + 1]);
+                m2 = fmaxf(m2, v[4 * j + 2]);
+                m3 = fmaxf(m3, v[4 * j + 3]);
+            }
+        }
+        for (; k + 192 < k1; k += 256) {
             m0 = fmaxf(m0, fabsf(row[k]));
             m1 = fmaxf(m1, fabsf(row[k + 64]));
             m2 = fmaxf(m2, fabsf(row[k + 128]));
@@ -339,6 +351,39 @@ __device__ __forceinline__ void load_panels_staged(const SliceDesc& d, float* ti
         }
 }
 
+// The same staging for rows that are not 16-byte aligned (or K % 4 != 0): instruction i loads
+// 128 contiguous bytes of each of 2 rows (lane L: row 2(i/4) + L/32, k = 32(i%4) + L%32), 64
+// scalar loads per lane in all, written to the tile one value at a time.
+__device__ __forceinline__ void load_panels_staged_scalar(const SliceDesc& d, float* tile, int item, int r0,
+                                                          int kpb, int lane, float (&x)[SPLIT_G][16]) {
+    const int kl = lane & 31;
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+        const int row = 2 * (i >> 2) + (lane >> 5);
+        v[i] = 0.0f;
+        if (r0 + row < d.R)
+            v[i] = d.src[(size_t)item * d.bstride + (size_t)(r0 + row) * d.ld + kpb * PANEL_K + 32 * (i & 3) + kl];
+    }
+#pragma unroll
+    for (int i = 0; i < 64; ++i)
+        tile[(2 * (i >> 2) + (lane >> 5)) * STAGE_PITCH + 32 * (i & 3) + kl] = v[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* src = tile + (lane & 31) * STAGE_PITCH + 16 * (lane >> 5);
+#pragma unroll
+    for (int g = 0; g < SPLIT_G; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = *reinterpret_cast<const float4*>(src + g * PANEL_K + 4 * q);
+            x[g][4 * q + 0] = t.x;
+            x[g][4 * q + 1] = t.y;
+            x[g][4 * q + 2] = t.z;
+            x[g][4 * q + 3] = t.w;
+        }
+}
+
 template <int S, bool INT32_OUT>
 __device__ void split_operand(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][32];
@@ -412,6 +457,8 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
         if (!d.strided && d.vec) {
             static_assert(SPLIT_G * PANEL_K == 128, "staged loads cover 2 rows x 128 k per instruction");
             load_panels_staged(d, stage + wv * 32 * STAGE_PITCH, item, r0, kpb, lane, x);
+        } else if (!d.strided) {
+            load_panels_staged_scalar(d, stage + wv * 32 * STAGE_PITCH, item, r0, kpb, lane, x);
         } else {
 #pragma unroll
             for (int g = 0; g < SPLIT_G; ++g) load_panel(d, kpb + g, rowp, h, false, x[g]);
@@ -845,8 +892,7 @@ void launch_absmax(const SliceDesc& a, const SliceDesc& b, hipStream_t stream) {
 
 void launch_split(const SliceDesc& a, const SliceDesc& b, int S, bool int32_out, hipStream_t stream) {
     const unsigned blocks = (unsigned)(a.split_blocks + b.split_blocks);
-    const bool staged = (a.split_blocks > 0 && !a.strided && a.vec) ||
-                        (b.split_blocks > 0 && !b.strided && b.vec);
+    const bool staged = (a.split_blocks > 0 && !a.strided) || (b.split_blocks > 0 && !b.strided);
     const size_t lds = staged ? 4 * 32 * STAGE_PITCH * sizeof(float) : 0;
     switch (S * 2 + (int32_out ? 1 : 0)) {
         case 2: split_kernel<1, false><<<blocks, 256, lds, stream>>>(a, b); break;
