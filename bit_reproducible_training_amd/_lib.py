@@ -106,6 +106,10 @@ _SIGNATURES = {
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),
                                           ctypes.POINTER(rg_layout_info)]),
+    "rg_test_block_order": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_void_p, ctypes.c_longlong,
+                                           ctypes.POINTER(ctypes.c_longlong)]),
     "rg_make_plan_strided_batched": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                     ctypes.c_int, ctypes.POINTER(rg_config),
                                                     ctypes.POINTER(rg_plan)]),

@@ -84,6 +84,32 @@ int blocks_per_cu(int ti, int tj, int S) {
     return std::max(1, std::min(2, (160 * 1024) / lds_bytes));
 }
 
+// Tile rows per group of the contraction's block order (block_tile): the power of two that
+// keeps the digit panels touched by one XCD's run of `chunk` consecutive tiles (row panels of
+// 64 ti rows, column panels of 64 tj columns) fewest. A run from the start of a group covers
+// that group column by column, then the next group.
+int group_rows(int chunk, int ti, int tj, int tiles_m, int tiles_n) {
+    int best_g = 1;
+    long long best = -1;
+    for (int g = 1; g <= tiles_m; g *= 2) {
+        long long left = std::min<long long>(chunk, (long long)tiles_m * tiles_n);
+        long long rows = 0, cols = 0;
+        for (int r0 = 0; r0 < tiles_m && left > 0; r0 += g) {
+            const int gr = std::min(g, tiles_m - r0);
+            const long long here = std::min<long long>(left, (long long)gr * tiles_n);
+            rows += std::min<long long>(gr, here);
+            cols = std::max<long long>(cols, (here + gr - 1) / gr);
+            left -= here;
+        }
+        const long long panels = rows * ti + cols * tj;
+        if (best < 0 || panels < best) {
+            best = panels;
+            best_g = g;
+        }
+    }
+    return best_g;
+}
+
 double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split, int S,
                  int num_cus, bool raw) {
     const double tiles = (double)ceil_div(M, 64 * ti) * ceil_div(N, 64 * tj) * batch;
@@ -237,6 +263,25 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
         L.Np = round_up(N, 64 * tj);
         L.split = std::min(split, nsteps);
         L.has_partial = L.split > 1 || extras.raw;
+        const int tiles_m = L.Mp / (64 * ti), tiles_n = L.Np / (64 * tj);
+        // The contraction's grid must fit the int block order (any workspace that fits in
+        // memory is far below this).
+        if ((long long)tiles_m * tiles_n * L.split * batch > (1ll << 31) - 1)
+            return hipErrorInvalidValue;
+        // Block order. With a multiple of 8 tile columns the hardware's dealing (workgroup i
+        // to XCD i mod 8) already keeps each XCD on tiles_n / 8 fixed tile columns for the
+        // whole grid, whose column panels then stay in its L2 from one round of blocks to the
+        // next when K is short; that plain order is kept (8192x3072x768: 2% faster than
+        // grouped). Otherwise an XCD's resident blocks take a run of consecutive tiles in
+        // groups of tile rows (N = 768 at 64x64: 1.5% faster; the LM head's 393 tile columns:
+        // 1%). Any order gives the same bits.
+        if (tiles_n % 8 == 0) {
+            L.xcd_chunk = 0;
+            L.group_m = 1;
+        } else {
+            L.xcd_chunk = std::max(1, dev.num_cus / 8) * blocks_per_cu(ti, tj, S);
+            L.group_m = group_rows(L.xcd_chunk, ti, tj, tiles_m, tiles_n);
+        }
     }
 
     const int rows_a = (int)std::min<long long>((long long)M * batch, 1 << 30);
@@ -518,6 +563,34 @@ int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950,
         info->Np = L.Np;
         info->Kp = L.Kp;
         info->split_k = L.split;
+    }
+    return hipSuccess;
+}
+
+int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
+                        int batch, int* coords, long long capacity, long long* blocks) {
+    if (!cfg || !blocks) return hipErrorInvalidValue;
+    rg::DeviceInfo dev{is_gfx950 != 0, num_cus};
+    rg::PlanExtras extras;
+    extras.batch = batch;
+    rg::Layout L;
+    int e = rg::plan_layout(M, N, K, cfg->split_k, cfg->tile_m, cfg->tile_n, cfg->algo,
+                            cfg->slices, cfg->trans_a != 0, cfg->trans_b != 0, dev, &L, extras);
+    if (e != hipSuccess) return e;
+    *blocks = 0;
+    if (L.algo == RG_ALGO_REFERENCE || L.small) return hipSuccess;
+    const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
+    const long long total = (long long)tiles_m * tiles_n * L.split * L.batch;
+    *blocks = total;
+    if (!coords || capacity < 4 * total) return hipSuccess;
+    for (long long i = 0; i < total; ++i) {
+        int item, part, tm, tn;
+        rg::block_tile(rg::xcd_order((int)i, (int)total, L.xcd_chunk), tiles_m, tiles_n, L.split,
+                       L.group_m, &item, &part, &tm, &tn);
+        coords[4 * i] = item;
+        coords[4 * i + 1] = part;
+        coords[4 * i + 2] = tm;
+        coords[4 * i + 3] = tn;
     }
     return hipSuccess;
 }

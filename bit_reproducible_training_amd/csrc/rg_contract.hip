@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, (contract_waves_per_simd<S, WT
 contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
               const int* __restrict__ eA, const int* __restrict__ eB, float* __restrict__ C,
               int64_t* __restrict__ partial, int M, int N, int Kp, int split, int tiles_n,
-              int Mp, int Np, long long ldc, long long c_item) {
+              int Mp, int Np, long long ldc, long long c_item, int xcd_chunk, int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)  // buffer resources exist only in the device pass
     constexpr int L = 2 * S - 1;
     constexpr int NW = WGM * WGN;                  // wavefronts per block
@@ -122,11 +122,17 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
-    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
-    const int part = blockIdx.y;
+    // The grid is (tiles, split, batch); which tile, part and item this block computes follows
+    // the XCD-aware block order (xcd_order, block_tile), a bijection of the grid's blocks.
+    int tm, tn, part, item;
+    {
+        const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int total = gridDim.x * gridDim.y * gridDim.z;
+        block_tile(xcd_order(lin, total, xcd_chunk), gridDim.x / tiles_n, tiles_n, split, group_m,
+                   &item, &part, &tm, &tn);
+    }
     // Item of a batch: its digit panels, exponents, output and partials follow the previous
-    // item's (blockIdx.z == 0 for a single GEMM).
-    const int item = blockIdx.z;
+    // item's (item 0 for a single GEMM).
     QA += (size_t)item * Mp * Kp * S;
     QB += (size_t)item * Np * Kp * S;
     eA += (size_t)item * Mp;
@@ -678,7 +684,7 @@ static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, c
     // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64, 64x128, 64x64 = 4 wavefronts;
     // 64x192 and 192x64 = 12 wavefronts of 32x32 (three per SIMD).
 #define RG_CONTRACT_ARGS qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n, L.Mp, L.Np, \
-                         out.ldc, out.c_item
+                         out.ldc, out.c_item, L.xcd_chunk, L.group_m
     // (The twelve-wavefront tiles exist for S = 3 only: their 48 stage panels split evenly over
     // 12 wavefronts; the planner never gives them to S < 3.)
     if constexpr (S == 3) {

@@ -85,6 +85,44 @@ constexpr int STEP_K = 64;  // k consumed per pipeline stage of the contraction
 // Longest K of the one-launch small-shape kernel (its digit panels of both operands sit in LDS).
 constexpr int SMALL_MAX_K = 512;
 
+// Which output tile a contraction block computes. The hardware deals a launch's workgroups to
+// the 8 XCDs in turn (linear workgroup id mod 8), and each XCD has its own L2. The block at
+// linear id `lin` (of `total`) computes logical block xcd_order(lin, total, chunk): an XCD's
+// successive workgroups take runs of `chunk` consecutive logical blocks (chunk = the blocks an
+// XCD holds at once), so the blocks resident on one XCD are neighbours in the logical order
+// and fetch their shared digit panels into that XCD's L2 once. A grid that is not a multiple
+// of 8 * chunk has its remainder dealt the same way with a smaller run, and its last
+// (total mod 8) blocks keep their own ids. chunk = 0 keeps every id (the plain row-major
+// order). The mapping is a bijection of [0, total).
+__host__ __device__ inline int xcd_order(int lin, int total, int chunk) {
+    if (chunk == 0) return lin;
+    const int full = total / (8 * chunk) * (8 * chunk);
+    const int xcd = lin & 7, loc = lin >> 3;
+    if (lin < full) return loc / chunk * (8 * chunk) + xcd * chunk + loc % chunk;
+    const int run = (total - full) / 8;  // full is a multiple of 8: lin & 7 is still the XCD
+    const int l2 = lin - full;
+    if (l2 < 8 * run) return full + xcd * run + (l2 >> 3);
+    return lin;
+}
+
+// Logical block t -> (item, split part, tile row, tile column). Logical blocks run item by
+// item, part by part; within a part, tiles go through groups of `group_m` tile rows (the last
+// group may be shorter), column by column inside a group, so a run of consecutive tiles covers
+// a few row panels of op(A) and a few column panels of op(B).
+__host__ __device__ inline void block_tile(int t, int tiles_m, int tiles_n, int split,
+                                           int group_m, int* item, int* part, int* tm, int* tn) {
+    const int tiles = tiles_m * tiles_n;
+    const int ip = t / tiles, tile = t - ip * tiles;
+    *item = ip / split;
+    *part = ip - *item * split;
+    const int span = group_m * tiles_n;
+    const int g = tile / span, w = tile - g * span;
+    const int left = tiles_m - g * group_m;
+    const int rows = left < group_m ? left : group_m;
+    *tm = g * group_m + w % rows;
+    *tn = w / rows;
+}
+
 // Where each region lives inside the caller's workspace, and how the work is split. A batch
 // of `batch` independent GEMMs of one shape stacks its items: item b's digit panels, exponents
 // and partial maxima follow item b-1's (per-item sizes Mp, Np), and its partials too.
@@ -96,6 +134,8 @@ struct Layout {
     int ti, tj;         // MFMA block tile = (64*ti) x (64*tj); 0 for REFERENCE and small
     bool small;         // one launch of contract_small (32x32 tiles, no workspace use)
     int split;          // split-K parts
+    int xcd_chunk;      // contraction block order (xcd_order): blocks resident per XCD, or 0
+    int group_m;        // tile rows per group of the block order (block_tile)
     bool ta, tb;
     bool a_strided, b_strided;  // operand read along k with a stride (column access)
     int nch_a, kch_a;   // row-max pass of op(A): chunks along K and chunk length

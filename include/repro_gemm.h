@@ -117,6 +117,17 @@ int rg_workspace_layout(int M, int N, int K, const rg_config* cfg, rg_layout_inf
 int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
                        rg_plan* plan, rg_layout_info* info);
 
+/* Test hook, no counterpart in the reference: which output tile each workgroup of the MFMA
+ * contraction computes, for the plan rg_plan_for_device makes (same arguments, batch items).
+ * *blocks receives the contraction's workgroup count (0 when the plan has no MFMA contraction:
+ * the reference algorithm or the one-launch small kernel). If coords is non-NULL and capacity
+ * >= 4 * *blocks, coords[4 i .. 4 i + 3] receives (item, split part, tile row, tile column)
+ * of the workgroup with linear id i (tiles of plan->tile_m x plan->tile_n); the hardware
+ * deals workgroup i to XCD i mod 8. Host only; 1 (invalid value) as rg_plan_for_device, or
+ * for batch outside 1..65535. */
+int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
+                        int batch, int* coords, long long capacity, long long* blocks);
+
 /* Test hook, no counterpart in the reference: the GPU epilogue's final rounding on arrays,
  * so tests can compare it with round_to_float on chosen inputs. Exactly one of levels and T
  * is non-NULL. levels: n x (2S-1) int32 level sums per output, most significant first, rounded
