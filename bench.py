@@ -41,9 +41,9 @@ STEADY_STEPS = 50
 # (profiles/contract_mfma_4096cube_traffic.md), measured on the contraction source whose SHA-256
 # is TRAFFIC_SOURCE_SHA256. A counter value cannot be read from inside this process, so the
 # figure is reported only while that source is unchanged; otherwise traffic is null.
-TRAFFIC_BYTES = 671469875
+TRAFFIC_BYTES = 671559680
 TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
-TRAFFIC_SOURCE_SHA256 = "e61b99c42d4196da1d69f70e60abaf613899f013bc4eef18939c59c02fcda2fb"
+TRAFFIC_SOURCE_SHA256 = "956485187151550da1b53fc3e6ff0556a029ea3e322ac18949e44d6d8c255a09"
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
