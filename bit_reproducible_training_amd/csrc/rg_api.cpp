@@ -75,7 +75,7 @@ void choose_chunks(int R, int rows, int K, bool strided, int* nch, int* kch) {
 // The per-tile constants (S = 3) were chosen so that the planner picks the fastest measured plan
 // on a sweep of every block tile x split over 22 shapes on MI355X (the GEMMs of BASELINE
 // configurations 3 and 5, squares, tall and long-K shapes; the GPU brought out of idle first):
-// 20 of the 22 picks are the fastest measured plan, the others within 2.2% and 10.5% of it. The
+// 21 of the 22 picks are the fastest measured plan, the other within 5.9% of it. The
 // stage time's MFMA part scales with S^2 for fewer slices.
 // Blocks of one MFMA tile resident per compute unit: the LDS ring (3 stages of the block's
 // digit panels) against 160 KiB, at most 2.
@@ -226,9 +226,10 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
         } else {
             tiles_cand[ntile][0] = 2; tiles_cand[ntile++][1] = 2;
             tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 1;
-            if (S == 3) {
-                tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 3;
+            if (S == 3) {  // 192x64 first: where the two tie (the same tile count), it was the
+                           // faster on every measured shape (the GPT-2 weight gradients, ~1.5%)
                 tiles_cand[ntile][0] = 3; tiles_cand[ntile++][1] = 1;
+                tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 3;
             }
         }
         const int split_lo = std::min(std::max(split_k, min_split), nsteps);

@@ -126,7 +126,7 @@ def test_split_raised_for_exact_int32(S, limit):
 
 def test_default_plan_follows_the_cost_model():
     """With the default split_k = 1 and tile hints, the planner picks the block tile (128x128,
-    64x64, and at S = 3 the twelve-wavefront 64x192 / 192x64) and split with the lowest
+    64x64, and at S = 3 the twelve-wavefront 192x64 / 64x192, in that order on a tie) and split with the lowest
     estimated time: waves of blocks over the GPU's block slots times the stages of a part, plus
     the int64 partials of a split. The cases below were measured on MI355X over every block tile
     x split, and the chosen plan was the fastest (512x512x8192 within 10.5%). An explicit split_k
@@ -135,10 +135,12 @@ def test_default_plan_follows_the_cost_model():
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 512)
     p, _ = _plan(1024, 64, 1024)          # 16 tiles of 64x64, 16 stages: split to fill a wave
     assert (p.tile_m, p.tile_n) == (64, 64) and p.split_k >= 8
-    p, _ = _plan(3072, 768, 8192, trans_a=True)   # 192 tiles of 64x192 = one wave, no partials
-    assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 1)
-    p, _ = _plan(768, 768, 8192, trans_a=True)    # 48 tiles of 64x192 x 5 parts
-    assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 5)
+    p, _ = _plan(3072, 768, 8192, trans_a=True)   # 192 tiles of 192x64 = one wave, no partials
+    assert (p.tile_m, p.tile_n, p.split_k) == (192, 64, 1)  # (64x192 ties: 192x64 measured faster)
+    p, _ = _plan(768, 3072, 8192, trans_a=True)
+    assert (p.tile_m, p.tile_n, p.split_k) == (192, 64, 1)
+    p, _ = _plan(768, 768, 8192, trans_a=True)    # 48 tiles of 192x64 x 5 parts
+    assert (p.tile_m, p.tile_n, p.split_k) == (192, 64, 5)
     p, _ = _plan(2304, 768, 8192, trans_a=True)   # 108 tiles of 128x128 x 2 parts
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 2)
     p, _ = _plan(8192, 768, 3072)         # 512 tiles of 64x192 = two waves of 48 stages
