@@ -915,9 +915,11 @@ def main():
                                       adv["C"] if adv else None)
     bit_exact = all(checks.values()) if checks else None
 
-    # The practical ceiling: sustained int8 MFMA rate with register operands (no memory),
-    # dense random bytes and zeros; the matrix cores' power draw depends on the operands.
+    # The practical ceiling: sustained int8 MFMA rate with register operands (no memory), on
+    # random bytes, on random bytes in [0, 127] (the lower digit planes' data) and on zeros; the
+    # matrix cores' power draw depends on the operands.
     ceiling = {"dense_tops": round(rg.measure_mfma_int8_rate(True), 1),
+               "low7_tops": round(rg.measure_mfma_int8_rate(low7=True), 1),
                "zero_tops": round(rg.measure_mfma_int8_rate(False), 1)}
 
     M = N = K = n
@@ -961,8 +963,10 @@ def main():
                              "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                              "bytes": slice_bytes},
-        "mfma_ceiling_measured": dict(ceiling, contract_frac_of_dense=round(
-            contract_tops / ceiling["dense_tops"], 4) if ceiling["dense_tops"] else None),
+        "mfma_ceiling_measured": dict(
+            ceiling,
+            contract_frac_of_dense=round(contract_tops / ceiling["dense_tops"], 4) if ceiling["dense_tops"] else None,
+            contract_frac_of_low7=round(contract_tops / ceiling["low7_tops"], 4) if ceiling["low7_tops"] else None),
         "cpu_baseline": cpu,
         "bit_exact": bit_exact,
         "checks": checks,

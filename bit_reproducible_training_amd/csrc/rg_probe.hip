@@ -1,7 +1,8 @@
 // Diagnostic: the sustained int8 MFMA rate of the current device, with operands held in
-// registers and no memory traffic in the loop. The dense-operand figure is the practical
-// ceiling for the contraction kernels under the device's power limit; zero operands show
-// how far data-dependent power lets the clock rise.
+// registers and no memory traffic in the loop. The random-byte and [0, 127]-byte figures are
+// practical ceilings for the contraction kernels under the device's power limit (the lower
+// digit planes are bytes in [0, 127]); zero operands show how far data-dependent power lets
+// the clock rise.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -43,7 +44,7 @@ __global__ void __launch_bounds__(256) mfma_probe(const v4i* __restrict__ in, in
 }  // namespace rg
 
 extern "C" int rg_measure_mfma_int8_rate(int dense, double* tops) {
-    if (!tops) return hipErrorInvalidValue;
+    if (!tops || dense < 0 || dense > 2) return hipErrorInvalidValue;
     int dev = 0, cus = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -59,7 +60,9 @@ extern "C" int rg_measure_mfma_int8_rate(int dense, double* tops) {
     for (int i = 0; i < rg::PROBE_WORDS; ++i)
         for (int j = 0; j < 4; ++j) {
             x = x * 6364136223846793005ull + 1442695040888963407ull;
-            host[i][j] = dense ? (int)(x >> 32) : 0;
+            const uint32_t bytes = (uint32_t)(x >> 32);
+            // 1: random bytes; 2: random bytes in [0, 127] (like the lower digit planes); 0: zeros
+            host[i][j] = dense == 0 ? 0 : (int)(dense == 2 ? bytes & 0x7F7F7F7Fu : bytes);
         }
     rg::v4i* din = nullptr;
     int* dout = nullptr;

@@ -138,11 +138,13 @@ def repro_gemm_strided_batched_fp32_ws(A, lda, stride_a, B, ldb, stride_b, C, ld
                                                workspace, int(workspace_bytes), stream)
 
 
-def measure_mfma_int8_rate(dense=True):
-    """Sustained int8 MFMA TOP/s of the current device with register operands (dense random
-    bytes or zeros); the practical ceiling of the contraction under the power limit."""
+def measure_mfma_int8_rate(dense=True, low7=False):
+    """Sustained int8 MFMA TOP/s of the current device with register operands: dense random
+    bytes, random bytes in [0, 127] (low7; the data of the lower digit planes) or zeros; the
+    practical ceiling of the contraction under the power limit."""
     out = ctypes.c_double()
-    _check(lib.rg_measure_mfma_int8_rate(int(bool(dense)), ctypes.byref(out)), "measure_mfma_int8_rate")
+    mode = 2 if low7 else int(bool(dense))
+    _check(lib.rg_measure_mfma_int8_rate(mode, ctypes.byref(out)), "measure_mfma_int8_rate")
     return out.value
 
 

@@ -171,9 +171,11 @@ int rg_gemm_fp32_noalloc(const float* A, const float* B, float* C, int M, int N,
 
 /* Diagnostic, no counterpart in the reference: the sustained int8 MFMA rate of the current
  * (gfx950) device in TOP/s, measured with a kernel that keeps its operands in registers
- * (no memory traffic) for about a millisecond. dense = 1: random operand bytes, the
- * practical ceiling of the contraction under the device's power limit; dense = 0: zero
- * operands. Allocates a few KiB of device memory and synchronises its own stream. */
+ * (no memory traffic) for about a millisecond. dense = 1: random operand bytes; dense = 2:
+ * random bytes in [0, 127] (as the contraction's lower digit planes); dense = 0: zero
+ * operands. The first two are practical ceilings of the contraction under the device's
+ * power limit. 1 (invalid value) for another dense. Allocates a few KiB of device memory and
+ * synchronises its own stream. */
 int rg_measure_mfma_int8_rate(int dense, double* tops);
 
 #ifdef __cplusplus

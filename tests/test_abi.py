@@ -243,3 +243,11 @@ def test_null_pointers_rejected_before_any_launch():
 
 def test_max_fixed_point_constant():
     assert math.isclose(127 * 128 ** 2 + 64 * 129, 2089024)
+
+
+def test_mfma_probe_rejects_unknown_operand_modes():
+    """rg_measure_mfma_int8_rate checks its arguments before touching a device."""
+    out = ctypes.c_double()
+    for mode in (-1, 3):
+        assert _lib.lib.rg_measure_mfma_int8_rate(mode, ctypes.byref(out)) == 1
+    assert _lib.lib.rg_measure_mfma_int8_rate(1, None) == 1
