@@ -18,6 +18,7 @@
 // Integer addition is associative, so the tile shape, the split and the order of k
 // never change T.
 #include "rg_internal.h"
+#include <type_traits>
 #include "repro_gemm_math.h"
 
 namespace rg {
@@ -112,8 +113,12 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     constexpr int PA = (BM / PANEL_ROWS) * 2 * S;  // A panels per stage
     constexpr int PB = (BN / PANEL_ROWS) * 2 * S;  // B panels per stage
     constexpr int PT = PA + PB;
-    constexpr int PW = PT / NW;                    // panels copied per wavefront per stage
-    static_assert(PT % NW == 0, "stage panels must split evenly over the wavefronts");
+    // Copies: with more than 4 wavefronts only wavefronts 0..3 (one per SIMD) issue the
+    // stage's copies, so a SIMD's other wavefronts never stall on the address unit's command
+    // queue and keep its matrix core fed while the copying one waits.
+    constexpr int CW = (NW > 4 && PT % 4 == 0) ? 4 : NW;  // copying wavefronts
+    constexpr int PW = PT / CW;                    // panels copied per copying wavefront per stage
+    static_assert(PT % CW == 0, "stage panels must split evenly over the copying wavefronts");
     static_assert(PW < 64, "vmcnt immediate");
     // Three-stage ring, filled by direct global->LDS loads (buffer_load_dwordx4 ... lds: lane
     // i's 16 bytes land at the wavefront-uniform LDS base + 16 i, which is the panel layout).
@@ -150,10 +155,12 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // (scalar registers); the only per-lane operand of the copies is lane * 16.
     const uint32_t step_bytes = 2u * S * PANEL_BYTES;
     const uint32_t part_bytes = (uint32_t)(s1 - s0) * step_bytes;
+    const bool copier = wave < CW;
     __amdgpu_buffer_rsrc_t rsrc[PW];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-        const int pi = wave + NW * i;
+        // (non-copying wavefronts never use rsrc)
+        const int pi = CW == NW ? wave + NW * i : (copier ? wave + CW * i : 0);
         const int8_t* base;
         if (pi < PA) {
             const int rl = pi / (2 * S), o = pi % (2 * S);
@@ -191,12 +198,17 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[l][ti][tj][e] = 0;
 
-    auto issue = [&](v4i (*slot)[64], int step) RG_INLINE {
-        const uint32_t soff = (uint32_t)(step - s0) * step_bytes;
+    // COPY (a std::integral_constant): whether this wavefront copies; the stage loop is
+    // instantiated once for copying and once for non-copying wavefronts, so neither version
+    // branches per stage.
+    auto issue = [&](v4i (*slot)[64], int step, auto copy) RG_INLINE {
+        if constexpr (decltype(copy)::value) {
+            const uint32_t soff = (uint32_t)(step - s0) * step_bytes;
 #pragma unroll
-        for (int i = 0; i < PW; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[i], RG_LDS_PTR(&slot[wave + NW * i][0]), 16, voff,
-                                                     soff, 0, 0);
+            for (int i = 0; i < PW; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[i], RG_LDS_PTR(&slot[wave + CW * i][0]), 16,
+                                                         voff, soff, 0, 0);
+        }
     };
     // One stage: two k-steps of 32. Digits are read in the order a0 b0 a1 b1 ... and each
     // digit product is issued as soon as both of its digits are in registers, with the reads
@@ -239,7 +251,8 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
 #pragma unroll
         for (int p = 0; p < S; ++p) mma(1, p, S - 1);
     };
-    auto compute = [&](v4i (*slot)[64], bool with_tail, v4i (*refill)[64], int s_refill, bool do_issue) RG_INLINE {
+    auto compute = [&](v4i (*slot)[64], bool with_tail, v4i (*refill)[64], int s_refill, bool do_issue,
+                       auto copy) RG_INLINE {
         if (with_tail) {
             mma(1, 0, S - 1);
             __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
@@ -250,9 +263,11 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
             mma(1, 1, S - 1);
             __builtin_amdgcn_sched_group_barrier(0x008, T, 0);
         }
-        if (do_issue) {
-            issue(refill, s_refill);
-            __builtin_amdgcn_sched_group_barrier(0x020, PW, 0);
+        if constexpr (decltype(copy)::value) {
+            if (do_issue) {
+                issue(refill, s_refill, copy);
+                __builtin_amdgcn_sched_group_barrier(0x020, PW, 0);
+            }
         }
         if (with_tail && S > 2) {
             mma(1, 2, S - 1);
@@ -297,31 +312,42 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
     // for its reads of stage s-1 (the deferred group's operands are in registers then),
     // barrier (everyone's stage s has landed and everyone's reads of stage s-1 are done, so
     // its slot can be refilled), contract stage s, issuing stage s+2 into that slot.
-    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s, bool do_issue, bool with_tail) RG_INLINE {
-        if (s + 1 < s1) RG_WAIT_VMCNT(PW);
-        else RG_WAIT_VMCNT(0);
+    auto stage = [&](v4i (*cur)[64], v4i (*refill)[64], int s, bool do_issue, bool with_tail,
+                     auto copy) RG_INLINE {
+        if constexpr (decltype(copy)::value) {
+            if (s + 1 < s1) RG_WAIT_VMCNT(PW);
+            else RG_WAIT_VMCNT(0);
+        }
         RG_WAIT_LGKMCNT0();
         // The hardware barrier, plus a compiler barrier for LDS accesses (the s_barrier
         // intrinsic alone does not keep memory operations from moving across it, and
         // __syncthreads() would also wait for the loads still in flight into other slots).
         asm volatile("s_barrier" ::: "memory");
-        compute(cur, with_tail, refill, s + 2, do_issue);
+        compute(cur, with_tail, refill, s + 2, do_issue, copy);
     };
 
-    if (s0 < s1) issue(lds[0], s0);
-    if (s0 + 1 < s1) issue(lds[1], s0 + 1);
     // The slot of stage s - 1 is the slot of stage s + 2. The first stage has nothing deferred;
     // the steady state issues and has a deferred group (no branches); the last two issue nothing.
-    int cur = 0, s = s0;
-    auto refill = [&]() RG_INLINE { return cur == 0 ? 2 : cur - 1; };
-    auto next = [&]() RG_INLINE { cur = cur == 2 ? 0 : cur + 1; ++s; };
-    if (s < s1) {
-        stage(lds[cur], lds[refill()], s, s + 2 < s1, false);
-        next();
+    auto pipeline = [&](auto copy) RG_INLINE {
+        if (s0 < s1) issue(lds[0], s0, copy);
+        if (s0 + 1 < s1) issue(lds[1], s0 + 1, copy);
+        int cur = 0, s = s0;
+        auto refill = [&]() RG_INLINE { return cur == 0 ? 2 : cur - 1; };
+        auto next = [&]() RG_INLINE { cur = cur == 2 ? 0 : cur + 1; ++s; };
+        if (s < s1) {
+            stage(lds[cur], lds[refill()], s, s + 2 < s1, false, copy);
+            next();
+        }
+        for (; s + 2 < s1; next()) stage(lds[cur], lds[refill()], s, true, true, copy);
+        for (; s < s1; next()) stage(lds[cur], lds[refill()], s, false, true, copy);
+        if (s0 < s1) tail();
+    };
+    if constexpr (CW == NW) {
+        pipeline(std::true_type());
+    } else {
+        if (copier) pipeline(std::true_type());
+        else pipeline(std::false_type());
     }
-    for (; s + 2 < s1; next()) stage(lds[cur], lds[refill()], s, true, true);
-    for (; s < s1; next()) stage(lds[cur], lds[refill()], s, false, true);
-    if (s0 < s1) tail();
 
     // Epilogue. Register e of a 32x32 accumulator tile holds row 8*(e/4) + 4*(lane/32) + e%4,
     // column lane%32.
