@@ -41,9 +41,9 @@ STEADY_STEPS = 50
 # (profiles/contract_mfma_4096cube_traffic.md), measured on the contraction source whose SHA-256
 # is TRAFFIC_SOURCE_SHA256. A counter value cannot be read from inside this process, so the
 # figure is reported only while that source is unchanged; otherwise traffic is null.
-TRAFFIC_BYTES = 671559680
+TRAFFIC_BYTES = 671612928
 TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
-TRAFFIC_SOURCE_SHA256 = "956485187151550da1b53fc3e6ff0556a029ea3e322ac18949e44d6d8c255a09"
+TRAFFIC_SOURCE_SHA256 = "2700b1bf51f4200572ee1abe103bc2fa480951fa00a601581d5b2f103e622d3b"
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
