@@ -117,7 +117,7 @@ double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split,
     const double slots = (double)std::max(1, num_cus) * per_cu;
     const double waves = std::ceil(tiles * split / slots);
     // per block wave at S = 3: 128x128 (8 wavefronts, one block per CU), 64x64 (4 wavefronts,
-    // two per CU), 64x192 and 192x64 (12 wavefronts), and the pinned-only 128x64 and 64x128
+    // two per CU), 64x192 and 192x64 (12 wavefronts), 128x64 and 64x128 (8 wavefronts of 32x32)
     double stage3 = 0.8, fixed_us = 3.0;
     if (ti == 2 && tj == 2) {
         stage3 = 1.276;
@@ -128,6 +128,9 @@ double plan_cost(int M, int N, int nsteps, int batch, int ti, int tj, int split,
     } else if (ti * tj == 3) {
         stage3 = 0.978;
         fixed_us = 9.66;
+    } else if (ti * tj == 2) {
+        stage3 = 0.704;
+        fixed_us = 8.5;
     }
     const double stage_us = 0.1 + (stage3 - 0.1) * (S * S / 9.0);
     const double steps = std::ceil((double)nsteps / split);
@@ -217,7 +220,7 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
         // that minimum, the next 8 splits and the splits that exactly fill 1..16 waves of the
         // GPU's block slots. The planner keeps the candidate with the lowest estimated time
         // (plan_cost); ties keep the earlier candidate.
-        int tiles_cand[4][2];
+        int tiles_cand[6][2];
         int ntile = 0;
         if (algo == RG_ALGO_TILED) {
             tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 1;
@@ -230,6 +233,9 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
                            // faster on every measured shape (the GPT-2 weight gradients, ~1.5%)
                 tiles_cand[ntile][0] = 3; tiles_cand[ntile++][1] = 1;
                 tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 3;
+                // the eight-wavefront 128x64 / 64x128 (costs fitted at S = 3 only)
+                tiles_cand[ntile][0] = 2; tiles_cand[ntile++][1] = 1;
+                tiles_cand[ntile][0] = 1; tiles_cand[ntile++][1] = 2;
             }
         }
         const int split_lo = std::min(std::max(split_k, min_split), nsteps);

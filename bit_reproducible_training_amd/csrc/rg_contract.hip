@@ -726,9 +726,9 @@ static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, c
     if (L.ti == 2 && L.tj == 2)
         contract_mfma<S, 2, 1, 2, 4><<<grid, 512, 0, stream>>>(RG_CONTRACT_ARGS);
     else if (L.ti == 2 && L.tj == 1)
-        contract_mfma<S, 2, 1, 2, 2><<<grid, 256, 0, stream>>>(RG_CONTRACT_ARGS);
+        contract_mfma<S, 1, 1, 4, 2><<<grid, 512, 0, stream>>>(RG_CONTRACT_ARGS);
     else if (L.ti == 1 && L.tj == 2)
-        contract_mfma<S, 1, 2, 2, 2><<<grid, 256, 0, stream>>>(RG_CONTRACT_ARGS);
+        contract_mfma<S, 1, 1, 2, 4><<<grid, 512, 0, stream>>>(RG_CONTRACT_ARGS);
     else
         contract_mfma<S, 1, 1, 2, 2><<<grid, 256, 0, stream>>>(RG_CONTRACT_ARGS);
 #undef RG_CONTRACT_ARGS

@@ -126,7 +126,8 @@ def test_split_raised_for_exact_int32(S, limit):
 
 def test_default_plan_follows_the_cost_model():
     """With the default split_k = 1 and tile hints, the planner picks the block tile (128x128,
-    64x64, and at S = 3 the twelve-wavefront 192x64 / 64x192, in that order on a tie) and split with the lowest
+    64x64, at S = 3 the twelve-wavefront 192x64 / 64x192, in that order on a tie, then the
+    eight-wavefront 128x64 / 64x128) and split with the lowest
     estimated time: waves of blocks over the GPU's block slots times the stages of a part, plus
     the int64 partials of a split. The cases below were measured on MI355X over every block tile
     x split, and the chosen plan was the fastest (512x512x8192 within 10.5%). An explicit split_k
@@ -141,8 +142,8 @@ def test_default_plan_follows_the_cost_model():
     assert (p.tile_m, p.tile_n, p.split_k) == (192, 64, 1)
     p, _ = _plan(768, 768, 8192, trans_a=True)    # 48 tiles of 192x64 x 5 parts
     assert (p.tile_m, p.tile_n, p.split_k) == (192, 64, 5)
-    p, _ = _plan(2304, 768, 8192, trans_a=True)   # 108 tiles of 128x128 x 2 parts
-    assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 2)
+    p, _ = _plan(2304, 768, 8192, trans_a=True)   # 216 tiles of 128x64 (8 wavefronts), no parts
+    assert (p.tile_m, p.tile_n, p.split_k) == (128, 64, 1)
     p, _ = _plan(8192, 768, 3072)         # 512 tiles of 64x192 = two waves of 48 stages
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 1)
     p, _ = _plan(1024, 1024, 65536)       # 64 tiles of 128x128, 1024 stages
