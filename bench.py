@@ -41,9 +41,9 @@ STEADY_STEPS = 50
 # (profiles/contract_mfma_4096cube_traffic.md), measured on the contraction source whose SHA-256
 # is TRAFFIC_SOURCE_SHA256. A counter value cannot be read from inside this process, so the
 # figure is reported only while that source is unchanged; otherwise traffic is null.
-TRAFFIC_BYTES = 671612928
+TRAFFIC_BYTES = 671606784
 TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
-TRAFFIC_SOURCE_SHA256 = "2700b1bf51f4200572ee1abe103bc2fa480951fa00a601581d5b2f103e622d3b"
+TRAFFIC_SOURCE_SHA256 = "e5cea0e1f15157a150fb610fa9b138d4961c8e349ed8712fa7b8807f7b4d01c7"
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
