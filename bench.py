@@ -43,7 +43,7 @@ STEADY_STEPS = 50
 # figure is reported only while that source is unchanged; otherwise traffic is null.
 TRAFFIC_BYTES = 671606784
 TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
-TRAFFIC_SOURCE_SHA256 = "e5cea0e1f15157a150fb610fa9b138d4961c8e349ed8712fa7b8807f7b4d01c7"
+TRAFFIC_SOURCE_SHA256 = "60d2d000bb07d1c92c9d3d0fc37d9e39ed8f3f73b8713483fb7d8b8e1893f40c"
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------

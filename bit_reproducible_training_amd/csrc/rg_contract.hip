@@ -707,8 +707,9 @@ static void launch_mfma_s(const Layout& L, const int8_t* qa, const int8_t* qb, c
                           hipStream_t stream) {
     const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)L.split, (unsigned)L.batch);
-    // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64, 64x128, 64x64 = 4 wavefronts;
-    // 64x192 and 192x64 = 12 wavefronts of 32x32 (three per SIMD).
+    // Block tiles: 128x128 = 8 wavefronts of 64x32; 128x64 and 64x128 = 8 wavefronts of 32x32
+    // (two per SIMD); 64x64 = 4 wavefronts of 32x32; 64x192 and 192x64 = 12 wavefronts of
+    // 32x32 (three per SIMD).
 #define RG_CONTRACT_ARGS qa, qb, ea, eb, C, partial, L.M, L.N, L.Kp, L.split, tiles_n, L.Mp, L.Np, \
                          out.ldc, out.c_item, L.xcd_chunk, L.group_m
     // (The twelve-wavefront tiles exist for S = 3 only: their 48 stage panels split evenly over

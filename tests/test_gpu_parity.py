@@ -82,6 +82,27 @@ def test_tile_and_split_invariance(torch_gpu):
             assert np.array_equal(bits(C), want), (tm, tn, split)
 
 
+@pytest.mark.parametrize("S", [1, 2])
+def test_eight_wave_half_tiles_low_slices(torch_gpu, S):
+    """The eight-wavefront 128x64 and 64x128 tiles pinned at S = 1 and 2 (the planner offers them
+    at S = 3 only), on ragged shapes, every transpose and splits 1 and 3."""
+    torch = torch_gpu
+    M, N, K = 333, 197, 1500
+    A = O.gen_normal(M * K, 1.0, 71 + S)
+    B = O.gen_normal(N * K, 0.3, 72 + S)
+    dA, dB = to_dev(torch, A), to_dev(torch, B)
+    ws = None
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        want = O.cpu_gemm(A, B, M, N, K, ta, tb, S).view(np.uint32)
+        for tm, tn in ((128, 64), (64, 128)):
+            for split in (1, 3):
+                note("half tiles S=%d %dx%d split %d ta=%d tb=%d" % (S, tm, tn, split, ta, tb))
+                cfg = rg.Config(tile_m=tm, tile_n=tn, split_k=split, slices=S, trans_a=ta, trans_b=tb)
+                C, plan, ws = run(torch, dA, dB, M, N, K, cfg, ws=ws)
+                assert (plan.tile_m, plan.tile_n) == (tm, tn)
+                assert np.array_equal(bits(C), want), (ta, tb, tm, tn, split)
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 def test_twelve_wave_tiles_ragged(torch_gpu, ta, tb):
     """The 64x192 and 192x64 tiles (S = 3) on shapes that are no multiple of 192 in either
