@@ -38,6 +38,7 @@ __device__ __forceinline__ RowScale row_scale(int se) {
 }
 
 __device__ __forceinline__ int round_fixed(float x, const RowScale& rs) {
+    if (!__builtin_isfinite(x)) return -rs.lim;  // NaN, +-inf: as repro_gemm::fixed_point
     const float v = (x * rs.p1) * rs.p2;
     const int X = (int)__builtin_rintf(v);  // v_rndne_f32: nearest-even; |v| < 2^22 here
     return min(max(X, -rs.lim), rs.lim);

@@ -7,7 +7,9 @@
 // C[M,N] = op(A)[M,K] * op(B)[K,N], FP32, row-major. The result is bit-identical across
 // runs, split_k values, tile sizes and GPUs, and equal to a CPU implementation of the same
 // definition. S=1: 7-bit inputs, 1 int8 product; S=2: 14-bit, 4; S=3: 21-bit, 9 (default).
-// Inputs must be finite. Do not build with -ffast-math or denormal flushing.
+// Inputs are meant to be finite; a NaN or an infinity still gives the bits of the reference's
+// CPU path (see fixed_point in repro_gemm_math.h). Do not build with -ffast-math or denormal
+// flushing.
 #include <hip/hip_runtime.h>
 
 #include <cstddef>

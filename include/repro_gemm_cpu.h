@@ -27,8 +27,9 @@
 //   2. T[r][c] = sum_k X[r][k] * Y[c][k] in int64 -- exact, so the order of k, the blocking
 //      and the threading cannot change it.
 //   3. C[r][c] = round_to_float(T[r][c], e_r + f_c - 14 (S - 1)).
-// Inputs must be finite (NaN and infinity have no fixed-point value; the GPU path has the same
-// contract).
+// Inputs are meant to be finite. For a NaN or an infinity the maxima skip NaN and fixed_point
+// gives -127 * 2^(7(S-1)), as the reference's CPU path does on x86; the GPU path gives the same
+// bits.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -91,15 +92,15 @@ inline double largest_fixed_point(int S) {
 
 // Fixed-point rows of an operand: R rows of K values, row r element k at
 // src[r * K + k] (row access) or src[k * R + r] (column access). Writes q[r * K + k] and
-// e[r]. Magnitudes are compared as the bit patterns of |x| (ordered like the values for
-// finite floats), which is the maximum the definition asks for.
+// e[r]. Magnitudes are compared as magnitude_key(x) (the bits of |x|, NaN skipped), which is
+// the maximum the definition asks for.
 inline void fixed_point_rows(const float* src, int R, int K, bool column_access, int S,
                              int32_t* q, int* e) {
     if (!column_access) {
         cpu_for(R, [&](int r) {
             const float* row = src + (size_t)r * K;
             uint32_t top = 0;
-            for (int k = 0; k < K; ++k) top = std::max(top, float_to_bits(row[k]) & 0x7FFFFFFFu);
+            for (int k = 0; k < K; ++k) top = std::max(top, magnitude_key(row[k]));
             const int ex = scale_exponent(bits_to_float(top));
             e[r] = ex;
             int32_t* out = q + (size_t)r * K;
@@ -116,7 +117,7 @@ inline void fixed_point_rows(const float* src, int R, int K, bool column_access,
         for (int k = 0; k < K; ++k) {
             const float* line = src + (size_t)k * R;
             for (int r = r0; r < r1; ++r)
-                top[r - r0] = std::max(top[r - r0], float_to_bits(line[r]) & 0x7FFFFFFFu);
+                top[r - r0] = std::max(top[r - r0], magnitude_key(line[r]));
         }
         int ex[CB];
         for (int r = r0; r < r1; ++r) e[r] = ex[r - r0] = scale_exponent(bits_to_float(top[r - r0]));

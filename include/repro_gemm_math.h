@@ -61,13 +61,25 @@ RG_HD inline int scale_exponent(float m) {
     return (f & (f - 1)) == 0 ? pf - 149 : pf - 148;
 }
 
+// Bits of |x|, ordered like the values for every non-NaN float, and 0 for a NaN: the largest
+// key of a row is the bit pattern of the maximum the reference takes with std::fmax, which
+// skips NaN (repro_gemm_cpu.h:30-31, 36-37).
+RG_HD inline uint32_t magnitude_key(float x) {
+    const uint32_t a = float_to_bits(x) & 0x7FFFFFFFu;
+    return a > 0x7F800000u ? 0u : a;
+}
+
 // X = round-to-nearest-even(x * 2^(7(S-1) - se)), clamped to |X| <= 127 * 2^(7(S-1))
 // (repro_gemm_math.cuh:71-83), computed on the integer significand of x.
-// Inputs must be finite (the reference's contract).
+// A NaN or infinite x gives -127 * 2^(7(S-1)). The definition is meant for finite inputs (the
+// reference's hash tool refuses others), but its CPU path still computes one: it converts
+// with (int)nearbyintf, which gives INT_MIN for a NaN or an infinity on x86, and then clamps.
+// Every path here gives that value, so the CPU and the GPU agree bit for bit on such inputs too.
 RG_HD inline int fixed_point(float x, int se, int S) {
     uint32_t b = float_to_bits(x);
     uint32_t be = (b >> 23) & 0xFFu, fr = b & 0x7FFFFFu;
     int64_t lim = (int64_t)127 << (7 * (S - 1));
+    if (be == 0xFFu) return (int)-lim;
     uint64_t mant = be ? (uint64_t)(fr | 0x800000u) : (uint64_t)fr;  // |x| = mant * 2^e2
     int e2 = be ? (int)be - 150 : -149;
     int up = e2 + 7 * (S - 1) - se;             // |x| * 2^(7(S-1)-se) = mant * 2^up

@@ -10,6 +10,7 @@
  */
 #include "repro_oracle.h"
 
+#include <limits.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
@@ -54,7 +55,9 @@ int oracle_scale_exponent(float m) {
  * (repro_gemm_math.cuh:71-83). */
 int oracle_fixed_point(float x, int se, int S) {
     float v = oracle_scale_by_pow2(x, 7 * (S - 1) - se);
-    int X = (int)nearbyintf(v);
+    /* The reference converts with (int)nearbyintf(v); for a NaN or an infinity that is INT_MIN
+     * on x86 (the "integer indefinite" of cvttss2si), stated here without the undefined cast. */
+    int X = isfinite(v) ? (int)nearbyintf(v) : INT_MIN;
     int lim = 127 << (7 * (S - 1));
     return X > lim ? lim : (X < -lim ? -lim : X);
 }

@@ -1,0 +1,51 @@
+"""GEMM inputs holding NaN or infinities on the GPU: every device route must give the bits of
+the reference's CPU path (the oracle), which maps a NaN or an infinity to -127 * 2^(7(S-1)) and
+skips NaN in the maxima (see tests/test_nonfinite.py). Routes: the one-launch small kernel, the
+one-pass slicing by rows and by columns with 64x64 and 128x128 tiles and split-K, the two-pass
+slicing past the one-pass K limit, the one-thread-per-output algorithm, and a strided batch."""
+import numpy as np
+import pytest
+
+import bit_reproducible_training_amd as rg
+from gpu_util import note, run, to_dev
+from oracle import oracle as O
+from test_nonfinite import TRANSPOSES, nonfinite_inputs
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # M, N, K, S, Config keyword arguments
+    (37, 29, 53, 3, {}),
+    (37, 29, 53, 1, {}),
+    (200, 150, 300, 3, dict(tile_m=64, tile_n=64)),
+    (200, 150, 300, 2, dict(tile_m=64, tile_n=64, split_k=3)),
+    (600, 520, 900, 3, dict(tile_m=128, tile_n=128)),
+    (300, 260, 5000, 3, dict(split_k=2)),
+    (90, 70, 400, 3, dict(algo=rg.Algo.Reference)),
+]
+
+
+@pytest.mark.parametrize("M,N,K,S,kw", CASES)
+def test_nonfinite_inputs_match_oracle(torch_gpu, M, N, K, S, kw):
+    torch = torch_gpu
+    A, B = nonfinite_inputs(M, N, K, 11 + K)
+    dA, dB = to_dev(torch, A), to_dev(torch, B)
+    ws = None
+    for ta, tb in TRANSPOSES:
+        want = O.cpu_gemm(A, B, M, N, K, ta, tb, S).view(np.uint32).ravel()
+        cfg = rg.Config(slices=S, trans_a=ta, trans_b=tb, **kw)
+        note("nonfinite", M, N, K, S, ta, tb, kw)
+        C, _, ws = run(torch, dA, dB, M, N, K, cfg, ws=ws)
+        assert np.array_equal(C.cpu().numpy().view(np.uint32).ravel(), want), (ta, tb)
+
+
+def test_nonfinite_batched_matches_oracle(torch_gpu):
+    torch = torch_gpu
+    batch, M, N, K = 3, 70, 50, 200
+    items = [nonfinite_inputs(M, N, K, 40 + b) for b in range(batch)]
+    A = torch.from_numpy(np.stack([a.reshape(M, K) for a, _ in items])).cuda()
+    B = torch.from_numpy(np.stack([b.reshape(N, K) for _, b in items])).cuda()
+    note("nonfinite batched", batch, M, N, K)
+    C = rg.bmm(A, B, tb=True).cpu().numpy()
+    for b, (a, bb) in enumerate(items):
+        want = O.cpu_gemm(a, bb, M, N, K, 0, 1, 3).view(np.uint32).ravel()
+        assert np.array_equal(C[b].view(np.uint32).ravel(), want), b
