@@ -18,7 +18,9 @@
  *                          integers), and against oracle/_ref (the reference header
  *                          compiled here) where that builds.
  *   oracle_fixed_point     exact rational arithmetic (Python fractions) on random and
- *                          edge inputs; oracle/_ref.
+ *                          edge inputs; oracle/_ref. NaN and infinite inputs (the x86
+ *                          conversion, -127 * 2^(7(S-1))): whole GEMMs against oracle/_ref
+ *                          and two GEMMs worked out by hand (tests/test_nonfinite.py).
  *   oracle_round_to_float  exact rational rounding to binary32 (Python ints) on
  *                          random, tie, subnormal-boundary and overflow inputs; _ref.
  *   oracle_cpu_gemm        the 21 GEMM output hashes the reference records for its
