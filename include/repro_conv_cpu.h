@@ -55,7 +55,10 @@ inline void require(bool ok, const char* what) {
     if (!ok) throw std::invalid_argument(what);
 }
 
-inline uint32_t magnitude_bits(float v) { return repro_gemm::float_to_bits(v) & 0x7FFFFFFFu; }
+// Ordering key of |v| for the maxima: its bits, with NaN skipped as in the GEMM (the
+// reference's convolution compares raw magnitude bits, so a NaN wins there; skipping it keeps
+// the convolution equal to the GEMM on its im2col matrix for every input, and equal to the GPU).
+inline uint32_t magnitude_bits(float v) { return repro_gemm::magnitude_key(v); }
 
 // Values of window w (= (n, oy, ox)) at every position k, zero in the padding.
 inline void gather_window(const float* x, const ConvShape& g, int w, float* vals) {

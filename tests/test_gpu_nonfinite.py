@@ -49,3 +49,23 @@ def test_nonfinite_batched_matches_oracle(torch_gpu):
     for b, (a, bb) in enumerate(items):
         want = O.cpu_gemm(a, bb, M, N, K, 0, 1, 3).view(np.uint32).ravel()
         assert np.array_equal(C[b].view(np.uint32).ravel(), want), b
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_nonfinite_convolution_matches_oracle(torch_gpu, S):
+    """Convolutions with NaN and infinities in x, w and dY, by the direct kernels, by the GEMM
+    pipeline and by the automatic choice: the oracle's bits (maxima skip NaN, a non-finite value
+    counts as -127 * 2^(7(S-1)))."""
+    from test_gpu_conv import RC, _run_algo
+    from test_nonfinite import CONV_SHAPE, conv_nonfinite_inputs, conv_oracle
+
+    torch = torch_gpu
+    for shape in (CONV_SHAPE, (4, 6, 14, 14, 16, 5, 5, 1, 1, 0, 0)):
+        x, w, dy = conv_nonfinite_inputs(shape, 50 + S + shape[1])
+        for kind, a, b in (("fwd", x, w), ("dX", dy, w), ("dW", dy, x)):
+            want = conv_oracle(kind, x, w, dy, shape, S).view(np.uint32).ravel()
+            algos = (RC.ALGO_GEMM, RC.ALGO_AUTO) if kind == "dW" else (RC.ALGO_DIRECT, RC.ALGO_GEMM, RC.ALGO_AUTO)
+            for algo in algos:
+                note("nonfinite conv", kind, shape, "S=%d algo=%d" % (S, algo))
+                got = _run_algo(torch, kind, a.ravel(), b.ravel(), shape, S, algo)
+                assert np.array_equal(got.view(np.uint32).ravel(), want), (kind, shape, algo)

@@ -74,3 +74,73 @@ def test_cpu_path_matches_oracle_on_nonfinite_inputs(S):
             want = O.cpu_gemm(A, B, M, N, K, ta, tb, S).view(np.uint32).ravel()
             got = rg.gemm(tA, tB, M, N, K, ta=bool(ta), tb=bool(tb), S=S).numpy().view(np.uint32).ravel()
             assert np.array_equal(got, want), (M, N, K, ta, tb)
+
+
+CONV_SHAPE = (2, 3, 9, 9, 4, 3, 3, 1, 1, 1, 1)
+
+
+def conv_nonfinite_inputs(shape, seed, nan=True):
+    """x, w and dy of a convolution with infinities (and, if nan, NaN) planted in each."""
+    rng = np.random.default_rng(seed)
+    N, C, H, W, F, KH, KW = shape[:7]
+    OH, OW = O.conv_out_hw(shape)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = rng.standard_normal((F, C, KH, KW)).astype(np.float32)
+    dy = rng.standard_normal((N, F, OH, OW)).astype(np.float32)
+    x[1, 0, 2, 7] = np.inf
+    x[1, C - 1, H - 1, 0] = -np.inf
+    dy[N - 1, 0, 1, 1] = np.inf
+    if nan:
+        x[0, 1, 4, 4] = np.nan
+        w[F // 2, 1, 0, KW - 1] = np.nan
+        dy[0, F - 1, OH // 2, OW // 2] = np.nan
+    return x, w, dy
+
+
+def _conv_cpu(kind, x, w, dy, shape, S):
+    import torch
+
+    import bit_reproducible_training_amd as rg
+
+    N, C, H, W, F, KH, KW, SY, SX, PY, PX = shape
+    t = torch.from_numpy
+    if kind == "fwd":
+        return rg.conv2d(t(x), t(w), SY, SX, PY, PX, S).numpy()
+    if kind == "dW":
+        return rg.conv2d_grad_weight(t(dy), t(x), KH, KW, SY, SX, PY, PX, S).numpy()
+    return rg.conv2d_grad_input(t(dy), t(w), (N, C, H, W), SY, SX, PY, PX, S).numpy()
+
+
+def conv_oracle(kind, x, w, dy, shape, S):
+    if kind == "fwd":
+        return O.conv2d(x, w, shape, S)
+    if kind == "dW":
+        return O.conv2d_grad_weight(dy, x, shape, S)
+    return O.conv2d_grad_input(dy, w, shape, S)
+
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32).ravel()
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_conv_cpu_path_matches_oracle_on_nonfinite_inputs(S):
+    """The convolution's maxima skip NaN as the GEMM's do (the reference's convolution lets a
+    NaN win its maxima, so it gives other bits where a NaN is present); infinities and the
+    -127 * 2^(7(S-1)) of a non-finite value are as in the GEMM."""
+    x, w, dy = conv_nonfinite_inputs(CONV_SHAPE, 20 + S)
+    for kind in ("fwd", "dW", "dX"):
+        assert np.array_equal(_bits(_conv_cpu(kind, x, w, dy, CONV_SHAPE, S)),
+                              _bits(conv_oracle(kind, x, w, dy, CONV_SHAPE, S))), kind
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_conv_oracle_matches_reference_with_infinities(S):
+    """With infinities and no NaN both kinds of maxima agree, so the oracle's convolution must
+    give the reference convolution's own bits (oracle/_ref)."""
+    if O.ref is None:
+        pytest.skip("oracle/_ref (the reference's CPU path) is not built here")
+    x, w, dy = conv_nonfinite_inputs(CONV_SHAPE, 30 + S, nan=False)
+    for kind, a, b in (("fwd", x, w), ("dW", dy, x), ("dX", dy, w)):
+        assert np.array_equal(_bits(O.ref_conv(kind, a, b, CONV_SHAPE, S)),
+                              _bits(conv_oracle(kind, x, w, dy, CONV_SHAPE, S))), kind
