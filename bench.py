@@ -36,14 +36,19 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 # The steady-state side measurement of the headline GEMM: GEMMs run first, then GEMMs timed.
 STEADY_WARM = 200
 STEADY_STEPS = 50
-# HBM bytes per launch of the contraction at 4096^3 S=3 (fetch + write), from rocprofv3
-# FETCH_SIZE / WRITE_SIZE scaled by the same counters on a 256 MiB device copy
-# (profiles/contract_mfma_4096cube_traffic.md), measured on the contraction source whose SHA-256
-# is TRAFFIC_SOURCE_SHA256. A counter value cannot be read from inside this process, so the
-# figure is reported only while that source is unchanged; otherwise traffic is null.
-TRAFFIC_BYTES = 671606784
-TRAFFIC_SOURCE = os.path.join(REPO, "bit_reproducible_training_amd", "csrc", "rg_contract.hip")
-TRAFFIC_SOURCE_SHA256 = "60d2d000bb07d1c92c9d3d0fc37d9e39ed8f3f73b8713483fb7d8b8e1893f40c"
+# HBM bytes per GEMM at 4096^3 S=3 (fetch + write) of the contraction launch and of the two
+# slicing launches, from rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by the same counters on a
+# 256 MiB device copy (profiles/contract_mfma_4096cube_traffic.md), each measured on the sources
+# whose SHA-256 (sources_digest) is given: the kernel file and rg_internal.h, which holds the
+# block order and the rounding helpers. A counter value cannot be read from inside this process,
+# so a figure is reported only while its sources are unchanged; otherwise it is null.
+CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
+TRAFFIC = {
+    "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
+                 "314465f63784c10e2681b472e1c4d752b2b2a1f862aa38448049b7802d7a17e5"),
+    "slicing": (303864832, ("rg_slice.hip", "rg_internal.h"),
+                "35b032e5bd52e4dacb081f1d1254d0477930f7f55ffe38c842de5a3141d55941"),
+}
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
 # --------------------------------------------------------------------------------------
@@ -53,16 +58,25 @@ FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 _G = np.uint64(0x9E3779B97F4A7C15)
 
 
-def measured_traffic():
-    """TRAFFIC_BYTES if the contraction source is the one it was measured on, else None."""
+def sources_digest(names):
+    """SHA-256 over the named files of csrc/, each as its name, a NUL byte and its bytes."""
     import hashlib
 
+    h = hashlib.sha256()
+    for name in names:
+        with open(os.path.join(CSRC, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
+def measured_traffic(stage="contract"):
+    """The measured HBM bytes per GEMM of a stage ("contract" or "slicing") if its sources are
+    the ones it was measured on, else None."""
+    nbytes, names, digest = TRAFFIC[stage]
     try:
-        with open(TRAFFIC_SOURCE, "rb") as f:
-            digest = hashlib.sha256(f.read()).hexdigest()
+        return nbytes if sources_digest(names) == digest else None
     except OSError:
         return None
-    return TRAFFIC_BYTES if digest == TRAFFIC_SOURCE_SHA256 else None
 
 
 def _draw(seed, idx):
@@ -927,6 +941,10 @@ def main():
     eff = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     int8_ops = S * S * 2.0 * M * N * K
     slice_bytes = 4 * (M * K + K * N) + S * (M * K + N * K) + 4 * (M + N)
+    # The measured traffic figures hold for the workload they were measured on only.
+    measured_shape = (M, N, K, S) == (4096, 4096, 4096, 3)
+    contract_traffic = measured_traffic("contract") if measured_shape else None
+    slice_traffic = measured_traffic("slicing") if measured_shape else None
     contract_tops = int8_ops / (head["contract_ms"] * 1e-3) / 1e12
     line = {
         "metric": "effective FP32 TFLOP/s, S=3 repro GEMM 4096^3; % int8 MFMA peak; bit-exact",
@@ -950,19 +968,24 @@ def main():
                       "final": round(head["final_ms"], 4)},
         "roofline": {"bound": "mfma", "achieved": round(contract_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(contract_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": measured_traffic(),
+                     "traffic": contract_traffic,
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, scaled by a "
                                        "256 MiB copy (profiles/contract_mfma_4096cube_traffic.md); "
-                                       "null when rg_contract.hip differs from the measured source",
+                                       "null when rg_contract.hip or rg_internal.h differs from the "
+                                       "measured sources",
                      "kernel": "contract_mfma<3,2,1,2,4>: int8 ops = 9 * 2MNK per launch, one "
                                "launch per step; achieved = ops / HIP-event duration"},
         # The slicing stage against the HBM roofline: algorithmic bytes = fp32 inputs read once
         # (4(MK + KN)) + S digit planes written (S(MK + NK)) + the int32 exponents (4(M + N)),
         # over the stage's HIP-event duration (both slicing launches and the gap between them).
+        # traffic: the launches' measured HBM bytes (B's column maxima read B a second time at
+        # this shape), and the rate they move them at.
         "slicing_roofline": {"bound": "hbm", "achieved": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9, 1),
                              "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                             "bytes": slice_bytes},
+                             "bytes": slice_bytes, "traffic": slice_traffic,
+                             "traffic_rate": (round(slice_traffic / (head["slice_ms"] * 1e-3) / 1e9, 1)
+                                              if slice_traffic else None)},
         "mfma_ceiling_measured": dict(
             ceiling,
             contract_frac_of_dense=round(contract_tops / ceiling["dense_tops"], 4) if ceiling["dense_tops"] else None,

@@ -23,17 +23,24 @@ def test_bench_normal_inputs_match_oracle_stream():
     assert np.array_equal(x.view(np.uint32), O.gen_normal(5000, 1.0, 7, 3).view(np.uint32))
 
 
-def test_traffic_reported_only_for_the_measured_contraction_source(tmp_path, monkeypatch):
-    """roofline.traffic is a rocprofv3 figure measured outside the run; bench.py gives it only
-    while the contraction source hashes to the one it was measured on."""
-    import hashlib
+def test_traffic_reported_only_for_the_measured_sources(tmp_path, monkeypatch):
+    """roofline.traffic and slicing_roofline.traffic are rocprofv3 figures measured outside the
+    run; bench.py gives each only while its sources hash to the ones it was measured on (a
+    change to either file, or a missing file, gives None)."""
+    (tmp_path / "k.hip").write_bytes(b"kernel v1")
+    (tmp_path / "h.h").write_bytes(b"helpers v1")
+    monkeypatch.setattr(bench, "CSRC", str(tmp_path))
+    digest = bench.sources_digest(("k.hip", "h.h"))
+    monkeypatch.setattr(bench, "TRAFFIC", {"contract": (123, ("k.hip", "h.h"), digest)})
+    assert bench.measured_traffic("contract") == 123
+    (tmp_path / "h.h").write_bytes(b"helpers v2")
+    assert bench.measured_traffic("contract") is None
+    (tmp_path / "h.h").write_bytes(b"helpers v1")
+    (tmp_path / "k.hip").write_bytes(b"kernel v2")
+    assert bench.measured_traffic("contract") is None
+    (tmp_path / "k.hip").unlink()
+    assert bench.measured_traffic("contract") is None
+    # the names are part of the digest: the same bytes under other names do not match
+    (tmp_path / "k2.hip").write_bytes(b"kernel v1")
+    assert bench.sources_digest(("k2.hip", "h.h")) != digest
 
-    src = tmp_path / "rg_contract.hip"
-    src.write_bytes(b"kernel v1")
-    monkeypatch.setattr(bench, "TRAFFIC_SOURCE", str(src))
-    monkeypatch.setattr(bench, "TRAFFIC_SOURCE_SHA256", hashlib.sha256(b"kernel v1").hexdigest())
-    assert bench.measured_traffic() == bench.TRAFFIC_BYTES
-    src.write_bytes(b"kernel v2")
-    assert bench.measured_traffic() is None
-    monkeypatch.setattr(bench, "TRAFFIC_SOURCE", str(tmp_path / "missing.hip"))
-    assert bench.measured_traffic() is None
