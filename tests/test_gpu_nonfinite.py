@@ -69,3 +69,32 @@ def test_nonfinite_convolution_matches_oracle(torch_gpu, S):
                 note("nonfinite conv", kind, shape, "S=%d algo=%d" % (S, algo))
                 got = _run_algo(torch, kind, a.ravel(), b.ravel(), shape, S, algo)
                 assert np.array_equal(got.view(np.uint32).ravel(), want), (kind, shape, algo)
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_random_shapes_and_plans_with_nonfinite_values(torch_gpu, chunk):
+    """The seeded random sweep of shapes and plans (tests/test_gpu_random_shapes.py) on inputs
+    with NaN, +inf and -inf sprinkled at random (about 1 in 200 values, and now and then a whole
+    row of A or column of B)."""
+    from test_gpu_random_shapes import _cases
+    from gpu_util import bits
+
+    torch = torch_gpu
+    for M, N, K, ta, tb, S, plan, _, seed in _cases(48, 2000 + chunk):
+        rng = np.random.default_rng(seed)
+        A, B = O.gen_hash_inputs(M, N, K, seed, "normal")
+        specials = np.array([np.nan, np.inf, -np.inf], np.float32)
+        for X in (A, B):
+            hit = rng.random(X.size) < 0.005
+            X.reshape(-1)[hit] = rng.choice(specials, int(hit.sum()))
+        if rng.random() < 0.3:
+            A.reshape(M, K)[int(rng.integers(0, M))] = rng.choice(specials)
+        if rng.random() < 0.3:
+            B.reshape(K, N)[:, int(rng.integers(0, N))] = rng.choice(specials)
+        want = O.cpu_gemm(A, B, M, N, K, 0, 0, S).view(np.uint32)
+        As = np.ascontiguousarray(A.reshape(M, K).T) if ta else A
+        Bs = np.ascontiguousarray(B.reshape(K, N).T) if tb else B
+        cfg = rg.Config(slices=S, trans_a=bool(ta), trans_b=bool(tb), **plan)
+        note("random nonfinite M=%d N=%d K=%d ta=%d tb=%d S=%d %s seed=%d" % (M, N, K, ta, tb, S, plan, seed))
+        C, got_plan, _ = run(torch, As.ravel(), Bs.ravel(), M, N, K, cfg)
+        assert np.array_equal(bits(C), want), (M, N, K, ta, tb, S, plan, seed, got_plan)
