@@ -46,8 +46,8 @@ CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
                  "314465f63784c10e2681b472e1c4d752b2b2a1f862aa38448049b7802d7a17e5"),
-    "slicing": (303864832, ("rg_slice.hip", "rg_internal.h"),
-                "35b032e5bd52e4dacb081f1d1254d0477930f7f55ffe38c842de5a3141d55941"),
+    "slicing": (303693824, ("rg_slice.hip", "rg_internal.h"),
+                "680058bf83c90e0c583fe452b8d529c60ad4c98c3805b1640d73a2378856ed6e"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
