@@ -102,6 +102,7 @@ _SIGNATURES = {
     "rg_test_round": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int,
                                      ctypes.c_void_p]),
+    "rg_test_set_spin_limit": (ctypes.c_int, [ctypes.c_int]),
     "rg_plan_for_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),

@@ -142,6 +142,7 @@ struct Layout {
     int nch_a, kch_a;   // row-max pass of op(A): chunks along K and chunk length
     int nch_b, kch_b;
     bool has_partial;
+    int ps_a, ps_b;     // parts of the one-read column slicing (pslice_route), 0 when not taken
     size_t qa, qb, ea, eb, pma, pmb, part, total;  // byte offsets, 256-aligned
 };
 
@@ -200,6 +201,22 @@ struct SliceDesc {
     long long max_blocks, split_blocks;
     int im2col;         // rows are gathered through `g` (one-pass route, row access, one item)
     Im2col g;
+    // One-read slicing of a column-access operand past the one-pass limit (launch_pslice): parts
+    // along K per 32-row panel (their partial maxima go to pmax[part], whose slots an earlier
+    // launch of the same call marks PM_EMPTY), the bound on a block's wait for the other parts,
+    // and the grid.
+    int ps_parts;
+    int spin_limit;
+    long long ps_blocks;
+};
+
+// Bit pattern of a partial-maximum slot not yet written by this call (a NaN; no maximum of
+// magnitudes is NaN, the maxima skip NaN).
+constexpr unsigned PM_EMPTY = 0xFFFFFFFFu;
+// A region of slots to mark PM_EMPTY.
+struct MarkRange {
+    unsigned* p = nullptr;
+    long long n = 0;
 };
 
 // Fills max_blocks / split_blocks of d.
@@ -215,6 +232,33 @@ constexpr int ONEPASS_MAX_K_COLUMNS = 3072;
 bool onepass_eligible(const SliceDesc& d);
 void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
                     hipStream_t stream);
+
+// One-read slicing of a column-access operand whose padded K is past the one-pass limit: a
+// block holds a 32-row panel of op(X) (32 columns of the stored matrix) over PS_NPB k panels
+// in registers, and the ps_parts blocks of a panel exchange their partial maxima.
+constexpr int PS_WAVES = 8;
+constexpr int PS_KPW = 4;                   // k panels per wavefront
+constexpr int PS_NPB = PS_WAVES * PS_KPW;   // k panels per block
+__host__ __device__ inline int pslice_parts(int Kp) { return (Kp / PANEL_K + PS_NPB - 1) / PS_NPB; }
+__host__ __device__ inline bool pslice_route(bool strided, int Kp) {
+    return strided && Kp > ONEPASS_MAX_K_COLUMNS;
+}
+// Polls of a block's wait for the other parts of its panel before it reads their k ranges
+// itself (rg_test_set_spin_limit sets it; the default is far past any normal wait; 0: no
+// exchange, every block reads its panel's whole K for the maxima).
+constexpr int DEFAULT_SPIN_LIMIT = 1 << 16;
+int slice_spin_limit();
+void set_slice_spin_limit(int polls);
+// Fills ps_parts / ps_blocks of d (spin_limit is the caller's).
+void pslice_grid(SliceDesc& d);
+// The partial-maximum slots the one read of d waits on.
+MarkRange pslice_slots(const SliceDesc& d);
+void launch_pslice(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
+                   hipStream_t stream);
+// One launch: the one read of `two` and the one pass of `one` (padded K <= ONEPASS_MAX_K).
+void launch_onepass_pslice(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream);
+// Marks two regions of slots PM_EMPTY (one small launch).
+void launch_mark(MarkRange a, MarkRange b, hipStream_t stream);
 // One launch: the one pass of `one` and the partial maxima of `two` (whose split follows).
 void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream);
 

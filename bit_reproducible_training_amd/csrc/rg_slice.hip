@@ -785,7 +785,7 @@ void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use
     const unsigned blocks = (unsigned)(na + nb);
     const int nf4 = onepass_nf4(kp);
 #define RG_ONEPASS(SS, NF)                                                                      \
-    (gather ? slice_onepass_kernel<SS, NF, false, true><<<blocks, 512, 0, stream>>>(a, b, na)    \
+    (gather ? slice_onepass_kernel<SS, NF, false, true><<<blocks, 512, 0, stream>>>(a, b, na) \
             : slice_onepass_kernel<SS, NF, false, false><<<blocks, 512, 0, stream>>>(a, b, na))
 #define RG_ONEPASS_S(SS)                                                                        \
     case SS * 100 + 3: RG_ONEPASS(SS, 3); break;                                                \
@@ -826,6 +826,244 @@ void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hi
     }
 #undef RG_FUSED_S
 #undef RG_FUSED
+}
+
+// One read of a column-access operand past the one-pass limit (element (r, k) of item b at
+// src[b*bstride + k*ld + r]). Block (rp, part) owns the 32-row panel rp of op(X) (32
+// neighbouring columns of the stored matrix) over the k panels [part*PS_NPB, (part+1)*PS_NPB):
+// wavefront w takes PS_KPW of them, lane L column L % 32 and the 16 k of half L / 32 of each, as
+// scalar loads (each load instruction reads two 128-byte k-row segments), and keeps them in
+// registers. The panel's row maxima need every part: each block publishes its 32 partial maxima
+// in its slots pmax[part][rows] and waits until the other parts' slots of the panel hold values
+// (an earlier launch of the same call marked every slot PM_EMPTY, so any other value in a slot
+// is this call's); then every block rounds its own values and writes their digit panels, so
+// the input is read once. The wait is bounded: a block that does not see every part's maxima
+// after spin_limit polls reads the panel's whole K itself for them (the same values: the
+// maximum is exact and order-free), so no block depends on another being resident or visible.
+// Part 0 writes the exponents.
+// Blocks run on XCD blk % 8 (the dispatcher deals workgroups to the XCDs in turn) and each XCD
+// takes a contiguous range of (panel, part) in panel order (ps_blocks is a multiple of 8), so a
+// panel's parts are dispatched one after another on one XCD, and the neighbouring panels of an
+// unaligned operand, which share the lines at their edges, run on one XCD too. The slots are
+// therefore written with plain stores, which land in the XCD's L2 (the compute unit's L1 is
+// write-through), and polled with non-temporal loads, which skip the L1 (where a polled line
+// would stay stale) and are served by that L2. A device-scope exchange instead goes to the
+// memory-side coherence point and, with acquire/release fences, writes back and invalidates the
+// XCD's whole L2 while the launch's other blocks fill it with digits. A block whose parts ran on
+// another XCD can only see PM_EMPTY or this call's maxima (the slots were marked by an earlier
+// launch, whose writes the launch boundary made visible everywhere), so at worst it takes the
+// fallback: placement never changes a bit.
+__device__ __forceinline__ unsigned load_bypass_l1(const unsigned* p) {
+    unsigned v;
+    asm volatile("global_load_dword %0, %1, off nt\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+
+__device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride, int part, int parts,
+                                               int spin_limit, int lane, float* mm) {
+    if (spin_limit <= 0) return false;
+    if (lane < 32) pm[(size_t)part * part_stride] = __float_as_uint(*mm);
+    for (int n = 0;; ++n) {
+        float m = *mm;
+        bool seen = true;
+        if (lane < 32)
+            for (int p = 0; p < parts; ++p) {
+                if (p == part) continue;
+                const unsigned v = load_bypass_l1(pm + (size_t)p * part_stride);
+                if (v == PM_EMPTY) seen = false;
+                else m = fmaxf(m, __uint_as_float(v));
+            }
+        if (__all(seen)) {
+            *mm = m;
+            return true;
+        }
+        if (n >= spin_limit) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+template <int S>
+__device__ void pslice_cols(const SliceDesc& d, long long blk) {
+    __shared__ float smax[16][32];
+    __shared__ float sfin[32];
+    __shared__ int sse[32];
+    __shared__ int sok;
+    const int npk = d.Kp / PANEL_K;
+    const int parts = d.ps_parts;
+    const long long rpanels = (long long)d.batch * (d.Rp / PANEL_ROWS);
+    const long long lin = (blk & 7) * (d.ps_blocks / 8) + (blk >> 3);
+    if (lin >= rpanels * parts) return;  // padding block (whole block)
+    const int rp = (int)(lin / parts), part = (int)(lin - (long long)rp * parts);
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int item = (rp * PANEL_ROWS) / d.Rp;
+    const int r0 = rp * PANEL_ROWS - item * d.Rp;  // the panel's first row within its item
+    const size_t rows_total = (size_t)d.batch * d.Rp;
+    const int r = r0 + (lane & 31), h = lane >> 5;
+    const int q = rp * PANEL_ROWS + (lane & 31);
+    const float* colp = d.src + (size_t)item * d.bstride + r;
+    const bool live = r < d.R;
+    const int kp0 = part * PS_NPB + wv * PS_KPW;
+    float x[PS_KPW][16];
+    if (live && (kp0 + PS_KPW) * PANEL_K <= d.K) {  // every value of this wavefront inside K
+#pragma unroll
+        for (int i = 0; i < PS_KPW; ++i) {
+            const float* p = colp + (size_t)((kp0 + i) * PANEL_K + 16 * h) * d.ld;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) x[i][j] = p[(size_t)j * d.ld];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PS_KPW; ++i) {
+            const int k0 = (kp0 + i) * PANEL_K + 16 * h;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                x[i][j] = (live && k0 + j < d.K) ? colp[(size_t)(k0 + j) * d.ld] : 0.0f;
+        }
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PS_KPW; ++i)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(x[i][j]));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane < 32) smax[wv][lane] = m;
+    __syncthreads();
+    if (wv == 0) {
+        float mm = 0.0f;
+        if (lane < 32) {
+            mm = smax[0][lane];
+#pragma unroll
+            for (int w = 1; w < PS_WAVES; ++w) mm = fmaxf(mm, smax[w][lane]);
+        }
+        int ok = 1;
+        if (parts > 1) {
+            unsigned* pm = reinterpret_cast<unsigned*>(d.pmax) + rp * PANEL_ROWS + (lane & 31);
+            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, &mm) ? 1 : 0;
+        }
+        if (lane < 32) sfin[lane] = mm;
+        if (lane == 0) sok = ok;
+    }
+    __syncthreads();
+    if (!sok) {  // the other parts' maxima were not all seen: the panel's maxima over all of K
+        const int c = t & 31, kph = t >> 5;  // 16 k phases of 32 columns
+        float mm = 0.0f;
+        if (r0 + c < d.R) {
+            const float* p = d.src + (size_t)item * d.bstride + r0 + c;
+            for (int k = kph; k < d.K; k += 16) mm = fmaxf(mm, fabsf(p[(size_t)k * d.ld]));
+        }
+        smax[kph][c] = mm;
+        __syncthreads();
+        if (t < 32) {
+            float f = smax[0][t];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) f = fmaxf(f, smax[i][t]);
+            sfin[t] = f;
+        }
+        __syncthreads();
+    }
+    if (t < 32) {
+        const int se = scale_exponent(sfin[t]);  // rows >= R have a zero maximum, so se == 0
+        sse[t] = se;
+        if (part == 0) d.expo[rp * PANEL_ROWS + t] = se;
+    }
+    __syncthreads();
+    const RowScale rs = row_scale<S>(sse[lane & 31]);
+#pragma unroll
+    for (int i = 0; i < PS_KPW; ++i)
+        if (kp0 + i < npk) emit_panel<S, false>(d, x[i], rs, rp, kp0 + i, q, h, lane);
+}
+
+template <int S>
+__global__ void __launch_bounds__(64 * PS_WAVES) pslice_kernel(SliceDesc a, SliceDesc b) {
+    const long long blk = blockIdx.x;
+    if (blk < a.ps_blocks) pslice_cols<S>(a, blk);
+    else pslice_cols<S>(b, blk - a.ps_blocks);
+}
+
+// The one read of operand `two` and the one pass of operand `one` in one launch (two's slots
+// marked by a launch before it), so that one's traffic keeps the memory busy while two's
+// blocks exchange their maxima. two's blocks come first.
+template <int S, int NF4>
+__global__ void __launch_bounds__(512) onepass_pslice_kernel(SliceDesc one, SliceDesc two) {
+    const long long blk = blockIdx.x;
+    if (blk < two.ps_blocks) pslice_cols<S>(two, blk);
+    else slice_onepass<S, NF4>(one, blk - two.ps_blocks);
+}
+
+// Marks the slots of m PM_EMPTY, spread over the launch's blocks.
+__device__ __forceinline__ void mark_slots(const MarkRange& m) {
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < m.n;
+         i += (long long)gridDim.x * blockDim.x)
+        m.p[i] = PM_EMPTY;
+}
+
+__global__ void __launch_bounds__(256) mark_kernel(MarkRange a, MarkRange b) {
+    mark_slots(a);
+    mark_slots(b);
+}
+
+namespace {
+int g_spin_limit = DEFAULT_SPIN_LIMIT;
+}
+
+int slice_spin_limit() { return g_spin_limit; }
+void set_slice_spin_limit(int polls) { g_spin_limit = polls < 0 ? 0 : polls; }
+
+void pslice_grid(SliceDesc& d) {
+    d.ps_parts = pslice_parts(d.Kp);
+    const long long units = (long long)d.batch * (d.Rp / PANEL_ROWS) * d.ps_parts;
+    d.ps_blocks = (units + 7) / 8 * 8;
+}
+
+MarkRange pslice_slots(const SliceDesc& d) {
+    MarkRange m;
+    if (d.ps_parts > 1) {
+        m.p = reinterpret_cast<unsigned*>(d.pmax);
+        m.n = (long long)d.ps_parts * d.batch * d.Rp;
+    }
+    return m;
+}
+
+void launch_pslice(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
+                   hipStream_t stream) {
+    SliceDesc x = a, y = b;
+    if (!use_a) x.ps_blocks = 0;
+    if (!use_b) y.ps_blocks = 0;
+    const unsigned blocks = (unsigned)(x.ps_blocks + y.ps_blocks);
+    if (blocks == 0) return;
+    switch (S) {
+        case 1: pslice_kernel<1><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y); break;
+        case 2: pslice_kernel<2><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y); break;
+        default: pslice_kernel<3><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y); break;
+    }
+}
+
+void launch_onepass_pslice(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream) {
+    const unsigned blocks = (unsigned)(onepass_blocks(one) + two.ps_blocks);
+#define RG_OPS(SS, NF) onepass_pslice_kernel<SS, NF><<<blocks, 512, 0, stream>>>(one, two)
+#define RG_OPS_S(SS)                                                                            \
+    case SS * 100 + 3: RG_OPS(SS, 3); break;                                                    \
+    case SS * 100 + 4: RG_OPS(SS, 4); break;                                                    \
+    case SS * 100 + 6: RG_OPS(SS, 6); break;                                                    \
+    case SS * 100 + 8: RG_OPS(SS, 8); break;                                                    \
+    case SS * 100 + 9: RG_OPS(SS, 9); break;                                                    \
+    case SS * 100 + 12: RG_OPS(SS, 12); break;                                                  \
+    case SS * 100 + 16: RG_OPS(SS, 16); break;
+    switch (S * 100 + onepass_nf4(one.Kp)) {
+        RG_OPS_S(1)
+        RG_OPS_S(2)
+        RG_OPS_S(3)
+        default: break;
+    }
+#undef RG_OPS_S
+#undef RG_OPS
+}
+
+void launch_mark(MarkRange a, MarkRange b, hipStream_t stream) {
+    const long long n = a.n + b.n;
+    if (n <= 0) return;
+    const long long blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+    mark_kernel<<<(unsigned)blocks, 256, 0, stream>>>(a, b);
 }
 
 // Grid sizes of the two passes for one operand.

@@ -138,6 +138,14 @@ int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950
 int rg_test_round(const int* levels, const long long* T, const int* E, float* out, long long n,
                   int S, void* stream);
 
+/* Test hook, no counterpart in the reference: the bound on a slicing block's wait for the
+ * other k ranges of its row panel (long column-access operands, whose blocks exchange partial
+ * maxima), in polls; past it the block reads the panel's whole K itself, which gives the same
+ * bits. Applies to launches made after the call. polls = 0 makes every such block take the
+ * fallback (tests of that path); a negative value restores the default. Returns the previous
+ * bound. Host only, process-wide. */
+int rg_test_set_spin_limit(int polls);
+
 /* Strided-batched GEMM, no counterpart in the reference (which lists it as still needed for
  * attention: README.md:29, repro_gemm_cuda/README.md:106). batch independent GEMMs
  *   C_b[M,N] = op(A_b) op(B_b),  A_b = A + b*stride_a, B_b = B + b*stride_b, C_b = C + b*stride_c
