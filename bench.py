@@ -650,6 +650,16 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
     sp = torch.cuda.current_stream().cuda_stream
     rows = []
     warm_gpu(torch, rg)
+    # What two stage events recorded back to back measure with no launch between them: taken off
+    # the stage times before the HBM rates below are computed.
+    fe = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    floor = []
+    for _ in range(20):
+        fe[0].record()
+        fe[1].record()
+        torch.cuda.synchronize()
+        floor.append(fe[0].elapsed_time(fe[1]))
+    event_floor_ms = statistics.median(floor)
     for name, M, N, K, ta, tb, S, sa, sb in _config_cases():
         if name == "c3.qkv.fwd":  # after the tiny LeNet GEMMs, which leave the GPU almost idle
             warm_gpu(torch, rg)
@@ -697,17 +707,31 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
         slice_ms, contract_ms, final_ms = (statistics.median(x[i] for x in stages) for i in range(3))
         graph_ms = round(_graph_ms(torch, step), 4) if ms < 0.1 else None
         flops = 2.0 * M * N * K
+        # Achieved HBM rates of the HBM-bound stages on their algorithmic bytes: the slicing
+        # reads 4(MK + KN) and writes S(MK + NK) digit bytes + 4(M + N) exponent bytes; the
+        # split-K reduction (plans with split > 1) reads 8 * split * MN int64 partials and writes
+        # 4MN bytes of C (at split 1 the rounding is fused into the contraction).
+        slice_bytes = 4 * (M * K + K * N) + S * (M * K + N * K) + 4 * (M + N)
+        final_bytes = 8 * plan.split_k * M * N + 4 * M * N if plan.split_k > 1 else None
+        small = plan.tile_m == 32  # one launch: the stage events bracket no slicing or reduction
         rows.append({"case": name, "M": M, "N": N, "K": K, "ta": ta, "tb": tb, "S": S,
                      "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "reps": reps,
                      "graph_ms": graph_ms,
                      "slice_ms": round(slice_ms, 4), "contract_ms": round(contract_ms, 4),
                      "final_ms": round(final_ms, 4),
+                     "slice_gbs": (None if small else
+                                   round(slice_bytes / (max(slice_ms - event_floor_ms, 1e-4) * 1e-3) / 1e9, 1)),
+                     "final_gbs": (round(final_bytes / (max(final_ms - event_floor_ms, 1e-4) * 1e-3) / 1e9, 1)
+                                   if final_bytes and not small else None),
                      "contract_int8_frac": round(S * S * flops / (contract_ms * 1e-3) / (PEAK_INT8_TOPS * 1e12), 4),
                      "plan": "%dx%d split %d" % (plan.tile_m, plan.tile_n, plan.split_k),
                      "repeat_bits_equal": bool(torch.equal(first.view(torch.int32), C.view(torch.int32)))})
         del dA, dB, ws, C, first
         torch.cuda.empty_cache()
     print(json.dumps({"mode": "configs", "data": "synthetic (torch.randn / uniform on the GPU, seed 2024)",
+                      "event_floor_ms": round(event_floor_ms, 4),
+                      "hbm_rates": "slice_gbs / final_gbs: algorithmic bytes over the stage time less "
+                                   "event_floor_ms, against 8000 GB/s",
                       "cases": rows}))
 
 

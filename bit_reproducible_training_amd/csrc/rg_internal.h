@@ -233,20 +233,33 @@ bool onepass_eligible(const SliceDesc& d);
 void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,
                     hipStream_t stream);
 
-// One-read slicing of a column-access operand whose padded K is past the one-pass limit: a
-// block holds a 32-row panel of op(X) (32 columns of the stored matrix) over PS_NPB k panels
-// in registers, and the ps_parts blocks of a panel exchange their partial maxima.
+// One-read slicing of an operand whose padded K is past the one-pass limit: a block holds a
+// 32-row panel of op(X) (column access: 32 columns of the stored matrix) over PS_NPB k panels,
+// or a strip of 8 rows (row access) over PS_ROW_NPB k panels, in registers, and the ps_parts
+// blocks of a panel or strip exchange their partial maxima.
 constexpr int PS_WAVES = 8;
-constexpr int PS_KPW = 4;                   // k panels per wavefront
-constexpr int PS_NPB = PS_WAVES * PS_KPW;   // k panels per block
-__host__ __device__ inline int pslice_parts(int Kp) { return (Kp / PANEL_K + PS_NPB - 1) / PS_NPB; }
+constexpr int PS_KPW = 4;                        // k panels per wavefront (column access)
+constexpr int PS_NPB = PS_WAVES * PS_KPW;        // k panels per block (column access)
+constexpr int PS_ROW_NF4 = 16;                   // k panels per wavefront (row access)
+constexpr int PS_ROW_NPB = PS_WAVES * PS_ROW_NF4;
+__host__ __device__ inline int pslice_parts(bool strided, int Kp) {
+    const int npb = strided ? PS_NPB : PS_ROW_NPB;
+    return (Kp / PANEL_K + npb - 1) / npb;
+}
+// At most this many parts per panel: the parts of a panel wait for each other, so they must be
+// resident together on one XCD (64 slots of this launch's blocks per XCD at S = 3); with 64 parts
+// they needed every slot at once and waited out their bound (measured: 1024x1024x65536 NN), with
+// 32 they did not. Longer operands (column access past K = 32768) keep the two passes.
+constexpr int PS_MAX_PARTS = 32;
 __host__ __device__ inline bool pslice_route(bool strided, int Kp) {
-    return strided && Kp > ONEPASS_MAX_K_COLUMNS;
+    return Kp > (strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K) &&
+           pslice_parts(strided, Kp) <= PS_MAX_PARTS;
 }
 // Polls of a block's wait for the other parts of its panel before it reads their k ranges
-// itself (rg_test_set_spin_limit sets it; the default is far past any normal wait; 0: no
-// exchange, every block reads its panel's whole K for the maxima).
-constexpr int DEFAULT_SPIN_LIMIT = 1 << 16;
+// itself (rg_test_set_spin_limit sets it; 0: no exchange, every block reads its panel's whole K
+// for the maxima). A poll takes about 0.45 us on MI355X, so the default bounds the wait near
+// 1 ms, far past a normal wait (parts that load together publish within a few tens of us).
+constexpr int DEFAULT_SPIN_LIMIT = 2048;
 int slice_spin_limit();
 void set_slice_spin_limit(int polls);
 // Fills ps_parts / ps_blocks of d (spin_limit is the caller's).
@@ -257,6 +270,8 @@ void launch_pslice(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_
                    hipStream_t stream);
 // One launch: the one read of `two` and the one pass of `one` (padded K <= ONEPASS_MAX_K).
 void launch_onepass_pslice(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream);
+// One launch: the one read of `ps` and the partial maxima of `two` (whose split follows).
+void launch_pslice_absmax(const SliceDesc& ps, const SliceDesc& two, int S, hipStream_t stream);
 // Marks two regions of slots PM_EMPTY (one small launch).
 void launch_mark(MarkRange a, MarkRange b, hipStream_t stream);
 // One launch: the one pass of `one` and the partial maxima of `two` (whose split follows).

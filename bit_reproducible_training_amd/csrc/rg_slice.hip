@@ -860,13 +860,13 @@ __device__ __forceinline__ unsigned load_bypass_l1(const unsigned* p) {
 }
 
 __device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride, int part, int parts,
-                                               int spin_limit, int lane, float* mm) {
+                                               int spin_limit, int lane, int nl, float* mm) {
     if (spin_limit <= 0) return false;
-    if (lane < 32) pm[(size_t)part * part_stride] = __float_as_uint(*mm);
+    if (lane < nl) pm[(size_t)part * part_stride] = __float_as_uint(*mm);
     for (int n = 0;; ++n) {
         float m = *mm;
         bool seen = true;
-        if (lane < 32)
+        if (lane < nl)
             for (int p = 0; p < parts; ++p) {
                 if (p == part) continue;
                 const unsigned v = load_bypass_l1(pm + (size_t)p * part_stride);
@@ -938,7 +938,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
         int ok = 1;
         if (parts > 1) {
             unsigned* pm = reinterpret_cast<unsigned*>(d.pmax) + rp * PANEL_ROWS + (lane & 31);
-            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, &mm) ? 1 : 0;
+            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, 32, &mm) ? 1 : 0;
         }
         if (lane < 32) sfin[lane] = mm;
         if (lane == 0) sok = ok;
@@ -973,11 +973,124 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
         if (kp0 + i < npk) emit_panel<S, false>(d, x[i], rs, rp, kp0 + i, q, h, lane);
 }
 
+// One read of a row-access operand past the one-pass limit (element (r, k) of item b at
+// src[b*bstride + r*ld + k]): block (strip, part) holds a strip of 8 rows over the k panels
+// [part*PS_ROW_NPB, (part+1)*PS_ROW_NPB) in registers, laid out as the one pass lays out its
+// strip (wavefront w: PS_ROW_NF4 k panels, lane L: row L/8 and k 4*(L%8)..+3 of each panel, 16-byte
+// loads), and exchanges its 8 partial maxima with the strip's other parts as pslice_cols does.
+template <int S>
+__device__ void pslice_rows(const SliceDesc& d, long long blk) {
+    __shared__ float smax[8][8];
+    __shared__ float sfin[8];
+    __shared__ int sse[8];
+    __shared__ int sok;
+    const int npk = d.Kp / PANEL_K;
+    const int parts = d.ps_parts;
+    const int per_item = d.Rp / 8;
+    const long long nstrips = (long long)d.batch * per_item;
+    const long long lin = (blk & 7) * (d.ps_blocks / 8) + (blk >> 3);
+    if (lin >= nstrips * parts) return;  // padding block (whole block)
+    const long long st = lin / parts;
+    const int part = (int)(lin - st * parts);
+    const int item = (int)(st / per_item);
+    const int r0 = (int)(st - (long long)item * per_item) * 8;  // first row within the item
+    const int rp = (item * d.Rp + r0) / PANEL_ROWS;              // stacked 32-row panel
+    const int r_in = r0 & 24;                                    // strip offset in the panel
+    const size_t rows_total = (size_t)d.batch * d.Rp;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const float* base = d.src + (size_t)item * d.bstride;
+    const int kp0 = part * PS_ROW_NPB + w * PS_ROW_NF4;
+    const int row = r0 + (lane >> 3);
+    float4 v[PS_ROW_NF4];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PS_ROW_NF4; ++i) {
+        const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
+        v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (row < d.R && k < d.K) {
+            const float* q = base + (size_t)row * d.ld + k;
+            if (d.vec) {
+                v[i] = *reinterpret_cast<const float4*>(q);
+            } else {  // unaligned rows or K % 4 != 0: four scalar loads inside K
+                v[i].x = q[0];
+                if (k + 1 < d.K) v[i].y = q[1];
+                if (k + 2 < d.K) v[i].z = q[2];
+                if (k + 3 < d.K) v[i].w = q[3];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PS_ROW_NF4; ++i) m = fmaxf(m, max4(v[i]));
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((lane & 7) == 0) smax[w][lane >> 3] = m;
+    __syncthreads();
+    if (w == 0) {
+        float mm = 0.0f;
+        if (lane < 8) {
+            mm = smax[0][lane];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) mm = fmaxf(mm, smax[i][lane]);
+        }
+        int ok = 1;
+        if (parts > 1) {
+            unsigned* pm = reinterpret_cast<unsigned*>(d.pmax) + (size_t)item * d.Rp + r0 + (lane & 7);
+            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, 8, &mm) ? 1 : 0;
+        }
+        if (lane < 8) sfin[lane] = mm;
+        if (lane == 0) sok = ok;
+    }
+    __syncthreads();
+    if (!sok) {  // the other parts' maxima were not all seen: wavefront w reads row r0 + w whole
+        float mm = 0.0f;
+        if (r0 + w < d.R) {
+            const float* q = base + (size_t)(r0 + w) * d.ld;
+            for (int k = lane; k < d.K; k += 64) mm = fmaxf(mm, fabsf(q[k]));
+        }
+        mm = wave_max(mm);
+        if (lane == 0) sfin[w] = mm;
+        __syncthreads();
+    }
+    if (t < 8) {
+        const int se = scale_exponent(sfin[t]);  // rows >= R have a zero maximum, so se == 0
+        sse[t] = se;
+        if (part == 0) d.expo[(size_t)item * d.Rp + r0 + t] = se;
+    }
+    __syncthreads();
+    uint32_t* out = static_cast<uint32_t*>(d.out);
+    const int ro = lane >> 3, h = (lane >> 2) & 1, wd = lane & 3;
+    const RowScale rs = row_scale<S>(sse[ro]);
+    uint32_t* o0 = out + (size_t)rp * npk * S * (PANEL_BYTES / 4) + 4 * (r_in + ro + 32 * h) + wd;
+#pragma unroll
+    for (int i = 0; i < PS_ROW_NF4; ++i) {
+        const int kp = kp0 + i;
+        if (kp >= npk) break;
+        const float x[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        int dg[S][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int dd[S];
+            digits_of<S>(round_fixed(x[j], rs), dd);
+#pragma unroll
+            for (int p = 0; p < S; ++p) dg[p][j] = dd[p];
+        }
+        uint32_t* o = o0 + (size_t)kp * S * (PANEL_BYTES / 4);
+#pragma unroll
+        for (int p = 0; p < S; ++p) o[p * (PANEL_BYTES / 4)] = pack4(dg[p][0], dg[p][1], dg[p][2], dg[p][3]);
+    }
+}
+
+template <int S>
+__device__ __forceinline__ void pslice_block(const SliceDesc& d, long long blk) {
+    if (d.strided) pslice_cols<S>(d, blk);
+    else pslice_rows<S>(d, blk);
+}
+
 template <int S>
 __global__ void __launch_bounds__(64 * PS_WAVES) pslice_kernel(SliceDesc a, SliceDesc b) {
     const long long blk = blockIdx.x;
-    if (blk < a.ps_blocks) pslice_cols<S>(a, blk);
-    else pslice_cols<S>(b, blk - a.ps_blocks);
+    if (blk < a.ps_blocks) pslice_block<S>(a, blk);
+    else pslice_block<S>(b, blk - a.ps_blocks);
 }
 
 // The one read of operand `two` and the one pass of operand `one` in one launch (two's slots
@@ -986,8 +1099,18 @@ __global__ void __launch_bounds__(64 * PS_WAVES) pslice_kernel(SliceDesc a, Slic
 template <int S, int NF4>
 __global__ void __launch_bounds__(512) onepass_pslice_kernel(SliceDesc one, SliceDesc two) {
     const long long blk = blockIdx.x;
-    if (blk < two.ps_blocks) pslice_cols<S>(two, blk);
+    if (blk < two.ps_blocks) pslice_block<S>(two, blk);
     else slice_onepass<S, NF4>(one, blk - two.ps_blocks);
+}
+
+// The one read of operand `ps` and the partial maxima (first of the two passes) of operand `two`
+// in one launch (ps's slots marked by a launch before it). ps's blocks come first.
+template <int S>
+__global__ void __launch_bounds__(512) pslice_absmax_kernel(SliceDesc ps, SliceDesc two) {
+    const long long blk = blockIdx.x;
+    if (blk < ps.ps_blocks) pslice_block<S>(ps, blk);
+    else if (two.strided) absmax_cols<8>(two, blk - ps.ps_blocks);
+    else absmax_rows<8>(two, blk - ps.ps_blocks);
 }
 
 // Marks the slots of m PM_EMPTY, spread over the launch's blocks.
@@ -1010,8 +1133,8 @@ int slice_spin_limit() { return g_spin_limit; }
 void set_slice_spin_limit(int polls) { g_spin_limit = polls < 0 ? 0 : polls; }
 
 void pslice_grid(SliceDesc& d) {
-    d.ps_parts = pslice_parts(d.Kp);
-    const long long units = (long long)d.batch * (d.Rp / PANEL_ROWS) * d.ps_parts;
+    d.ps_parts = pslice_parts(d.strided != 0, d.Kp);
+    const long long units = (long long)d.batch * (d.Rp / (d.strided ? PANEL_ROWS : 8)) * d.ps_parts;
     d.ps_blocks = (units + 7) / 8 * 8;
 }
 
@@ -1057,6 +1180,15 @@ void launch_onepass_pslice(const SliceDesc& one, const SliceDesc& two, int S, hi
     }
 #undef RG_OPS_S
 #undef RG_OPS
+}
+
+void launch_pslice_absmax(const SliceDesc& ps, const SliceDesc& two, int S, hipStream_t stream) {
+    const unsigned blocks = (unsigned)(ps.ps_blocks + absmax8_blocks(two));
+    switch (S) {
+        case 1: pslice_absmax_kernel<1><<<blocks, 512, 0, stream>>>(ps, two); break;
+        case 2: pslice_absmax_kernel<2><<<blocks, 512, 0, stream>>>(ps, two); break;
+        default: pslice_absmax_kernel<3><<<blocks, 512, 0, stream>>>(ps, two); break;
+    }
 }
 
 void launch_mark(MarkRange a, MarkRange b, hipStream_t stream) {

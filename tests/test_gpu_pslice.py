@@ -1,14 +1,15 @@
-"""The one-read slicing of long column-access operands (launch_pslice) on the GPU.
+"""The one-read slicing of long operands (launch_pslice) on the GPU.
 
-An operand read along columns (op(B) of an NN or TN GEMM, op(A) of a TN or TT GEMM) whose
-padded K is past the one-pass limit is read once: blocks hold a 32-column panel over a range of
-k in registers and the panel's blocks exchange their partial maxima through a counter in the
-workspace. Checked against the oracle: every digit of both operands' panels, the exponents, the
-zero padding and the GEMM's bits, at S = 1..3, over every transpose, for K just past the limit,
-K with a partial last part, ragged panels and long K; the same with the wait bound set to zero
-(every block then reads its panel's whole K itself for the maxima, the fallback that keeps a
-block from depending on another being resident); on a workspace of random bytes (the counters
-must be cleared by the call itself); and in strided batches.
+An operand whose padded K is past the one-pass limit (column access: op(B) of an NN or TN GEMM,
+op(A) of a TN or TT GEMM, past 3072; row access past 4096) is read once: blocks hold a 32-column
+panel or an 8-row strip over a range of k in registers, and the blocks of a panel exchange their
+partial maxima through slots in the workspace that the call marks empty first. Checked against
+the oracle: every digit of both operands' panels, the exponents, the zero padding and the
+GEMM's bits, at S = 1..3, over every transpose, for K just past the limits, K with a partial
+last part, ragged panels and long K; the same with the wait bound set to zero (every block then
+reads its panel's whole K itself for the maxima, the fallback that keeps a block from depending
+on another being resident or visible); on a workspace of constant bytes (the slots must be
+marked by the call itself); and in strided batches.
 """
 import numpy as np
 import pytest
@@ -22,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 # Padded K from just past the column one-pass limit (3072) to several parts of 1024 k.
 SHAPES = [(64, 100, 3076), (33, 200, 4096), (100, 33, 5000), (130, 70, 8193), (32, 32, 3073),
-          (70, 45, 4097)]
+          (70, 45, 4097), (24, 40, 12289), (9, 17, 20000)]
 
 
 def _check_slices(torch, A, B, M, N, K, ta, tb, S, ws_fill=None):
@@ -60,7 +61,7 @@ def _inputs(M, N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
-@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (1, 1)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 @pytest.mark.parametrize("S", [1, 2, 3])
 def test_one_read_slicing_against_oracle(torch_gpu, M, N, K, ta, tb, S):
     A, B = _inputs(M, N, K, M * 3 + N * 7 + K + 11 * ta + 5 * tb + S)
@@ -69,7 +70,8 @@ def test_one_read_slicing_against_oracle(torch_gpu, M, N, K, ta, tb, S):
 
 
 @pytest.mark.parametrize("M,N,K,ta,tb", [(64, 100, 3076, 0, 0), (130, 70, 8193, 1, 0),
-                                         (100, 33, 5000, 1, 1)])
+                                         (100, 33, 5000, 1, 1), (40, 70, 9000, 0, 1),
+                                         (33, 20, 17000, 0, 0)])
 def test_one_read_slicing_fallback(torch_gpu, M, N, K, ta, tb):
     """Wait bound 0: every block takes the fallback; same digits and bits."""
     A, B = _inputs(M, N, K, 99 + K)
@@ -83,11 +85,11 @@ def test_one_read_slicing_fallback(torch_gpu, M, N, K, ta, tb):
 
 @pytest.mark.parametrize("fill", [0xFF, 0x01])
 def test_one_read_slicing_on_garbage_workspace(torch_gpu, fill):
-    """The counters start from whatever the workspace holds: the call clears them itself, both
-    when the other operand takes the one pass (cleared by that launch) and when both take the
-    one read (a launch of their own)."""
+    """The partial-maximum slots start from whatever the workspace holds (a constant fill can look
+    like a published maximum): the call marks them empty itself before the one read, whether the
+    other operand takes the one pass in the same launch or the one read too."""
     torch = torch_gpu
-    for M, N, K, ta, tb in [(96, 64, 4100, 0, 0), (64, 96, 6000, 1, 0)]:
+    for M, N, K, ta, tb in [(96, 64, 4100, 0, 0), (64, 96, 6000, 1, 0), (64, 96, 6000, 0, 1)]:
         A, B = _inputs(M, N, K, fill + K)
         for rep in range(2):
             note("pslice garbage fill=%d M=%d N=%d K=%d ta=%d tb=%d rep %d" % (fill, M, N, K, ta, tb, rep))
@@ -95,8 +97,8 @@ def test_one_read_slicing_on_garbage_workspace(torch_gpu, fill):
 
 
 def test_one_read_slicing_repeated_calls_one_workspace(torch_gpu):
-    """Back-to-back calls on one workspace (the counters left by one call are cleared by the
-    next), different inputs each time."""
+    """Back-to-back calls on one workspace, different inputs each time: the maxima a call leaves
+    in the slots must never be taken for the next call's."""
     torch = torch_gpu
     M, N, K = 200, 160, 4500
     cfg = rg.Config(slices=3)
@@ -118,11 +120,11 @@ def test_one_read_slicing_repeated_calls_one_workspace(torch_gpu):
         assert np.array_equal(bits(C), want)
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0)])
-def test_one_read_slicing_batched(torch_gpu, ta, tb):
+@pytest.mark.parametrize("ta,tb,K", [(0, 0, 4000), (1, 0, 4000), (0, 1, 6000)])
+def test_one_read_slicing_batched(torch_gpu, ta, tb, K):
     torch = torch_gpu
-    rng = np.random.default_rng(7 + ta)
-    batch, M, N, K = 3, 45, 70, 4000
+    rng = np.random.default_rng(7 + ta + K)
+    batch, M, N = 3, 45, 70
     a_shape = (batch, K, M) if ta else (batch, M, K)
     b_shape = (batch, N, K) if tb else (batch, K, N)
     A = (rng.standard_normal(a_shape) * 2.0 ** rng.integers(-20, 20, (batch, 1, 1))).astype(np.float32)
