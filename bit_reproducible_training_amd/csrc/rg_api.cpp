@@ -160,6 +160,10 @@ bool small_path(int M, int N, int K, int batch, int split_k, int tile_m, int til
                 const PlanExtras& extras, int num_cus) {
     if (algo == RG_ALGO_TILED || split_k != 1 || K > SMALL_MAX_K) return false;
     if (!extras.one_launch || extras.raw || !extras.gemm_bound) return false;
+    // A launch dimension holds fewer than 2^32 work-items: the kernel's grid is one block of
+    // SMALL_THREADS per 32x32 tile, so a pinned 32x32 tile beyond that takes the pipeline.
+    const long long tiles32 = (long long)ceil_div(M, 32) * ceil_div(N, 32);
+    if (tiles32 * SMALL_THREADS >= (1ll << 32)) return false;
     if (tile_m == 32 && tile_n == 32) return true;
     if (pinned_tile(tile_m, tile_n, 3)) return false;
     const double tiles = (double)ceil_div(M, 32) * ceil_div(N, 32) * batch;
@@ -529,26 +533,30 @@ static __device__ __align__(256) unsigned char scratch[RG_NOALLOC_SCRATCH_BYTES]
 namespace {
 
 struct ScratchSlot {
-    std::once_flag once;
-    void* ptr = nullptr;
-    int err = hipSuccess;
+    std::atomic<void*> ptr{nullptr};
+    std::mutex mu;
 };
 ScratchSlot g_scratch[64];
 
-// The scratch array's address on the current device (looked up on the first call per device).
+// The scratch array's address on the current device, looked up on the first successful call per
+// device and kept; a failed lookup is returned and not kept, so a later call tries again.
 int scratch_on_current_device(void** out) {
     int dev = 0;
     int e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     ScratchSlot& slot = g_scratch[dev];
-    std::call_once(slot.once, [&slot]() {
-        void* p = nullptr;
-        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        slot.ptr = slot.err == hipSuccess ? p : nullptr;
-    });
-    if (slot.err != hipSuccess) return slot.err;
-    *out = slot.ptr;
+    void* p = slot.ptr.load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(slot.mu);
+        p = slot.ptr.load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+            if (p == nullptr) return hipErrorInvalidSymbol;
+            slot.ptr.store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
     return hipSuccess;
 }
 

@@ -449,7 +449,6 @@ struct SmallOperand {
     int vec;
 };
 
-constexpr int SMALL_THREADS = 1024;
 constexpr int SMALL_SLOTS = 2 * (SMALL_MAX_K / PANEL_K) * 64 / SMALL_THREADS;  // per thread, at most
 
 template <int S>

@@ -85,6 +85,8 @@ constexpr int PANEL_BYTES = 1024;
 constexpr int STEP_K = 64;  // k consumed per pipeline stage of the contraction
 // Longest K of the one-launch small-shape kernel (its digit panels of both operands sit in LDS).
 constexpr int SMALL_MAX_K = 512;
+// Threads of a block of the one-launch small-shape kernel (one block per 32x32 tile of C).
+constexpr int SMALL_THREADS = 1024;
 
 // Which output tile a contraction block computes. The hardware deals a launch's workgroups to
 // the 8 XCDs in turn (linear workgroup id mod 8), and each XCD has its own L2. The block at

@@ -194,10 +194,13 @@ def bmm(A, B, ta=False, tb=False, S=3, cfg=None, out=None):
     item of a [T, H * D] activation): the library reads them in place through leading
     dimensions and batch strides. A batch dimension of size 1 broadcasts. C is [batch, M, N];
     out, if given, must be a float32 [batch, M, N] tensor on A's device with a contiguous last
-    dimension. CPU tensors run gemm() item by item.
+    dimension. CPU tensors run gemm() item by item. cfg (a Config), if given, replaces ta, tb and
+    S as in gemm(): the shapes are read with cfg's transposes.
     """
     import torch
 
+    if cfg is not None:
+        ta, tb = bool(cfg.trans_a), bool(cfg.trans_b)
     if A.dim() != 3 or B.dim() != 3:
         raise ValueError("bmm: A and B must be 3-D")
     if A.dtype != torch.float32 or B.dtype != torch.float32:

@@ -195,6 +195,12 @@ def test_small_shapes_take_the_one_launch_kernel():
     assert (p.tile_m, p.tile_n) == (32, 32)
     p, _ = _plan(64, 64, 1024, tile_m=32, tile_n=32)      # pinned, but K too long: planner's choice
     assert (p.tile_m, p.tile_n) != (32, 32)
+    # pinned, but 2^22 tiles of 1024 threads would not fit one launch dimension (2^32 work-items):
+    # the pipeline, whose grid fits
+    p, _ = _plan(65536, 65536, 256, tile_m=32, tile_n=32)
+    assert (p.tile_m, p.tile_n) != (32, 32) and p.algo == rg.Algo.TensorCore
+    p, _ = _plan(65536, 65504, 256, tile_m=32, tile_n=32)  # one tile column fewer: still fits
+    assert (p.tile_m, p.tile_n) == (32, 32)
 
 
 def test_split_clamped_to_k_steps():

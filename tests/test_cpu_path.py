@@ -337,6 +337,28 @@ def test_binding_cpu_gemm_and_checks(ch):
         rg.gemm(A, B, 6, 4, 5, S=4)
 
 
+def test_bmm_cpu_takes_transposes_from_cfg():
+    """bmm(..., cfg=Config(trans_b=True)) reads B as [batch, N, K], as gemm() takes cfg's
+    transposes; a layout that does not match cfg is refused rather than read out of bounds."""
+    import torch
+
+    import bit_reproducible_training_amd as rg
+
+    batch, M, N, K = 2, 5, 7, 9
+    for ta, tb in ((0, 1), (1, 0), (1, 1)):
+        A = torch.randn(batch, K, M) if ta else torch.randn(batch, M, K)
+        B = torch.randn(batch, N, K) if tb else torch.randn(batch, K, N)
+        cfg = rg.Config(trans_a=bool(ta), trans_b=bool(tb))
+        C = rg.bmm(A, B, cfg=cfg)  # ta, tb left at their defaults: cfg decides
+        assert tuple(C.shape) == (batch, M, N)
+        for i in range(batch):
+            want = O.cpu_gemm(A[i].numpy(), B[i].numpy(), M, N, K, ta, tb, 3)
+            assert np.array_equal(bits(C[i].numpy()), bits(want))
+    # A [1, 2, 8] with cfg.trans_a: op(A) is 8 x 2, so K = 2 and B [1, 8, 4] does not match
+    with pytest.raises(ValueError):
+        rg.bmm(torch.randn(1, 2, 8), torch.randn(1, 8, 4), cfg=rg.Config(trans_a=True))
+
+
 def test_binding_cpu_sum_conv_scan():
     import torch
 

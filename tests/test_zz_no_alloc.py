@@ -61,6 +61,20 @@ def test_noalloc_matches_workspace_entry_point(torch_gpu, first, second):
             assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
+def test_noalloc_first_call_under_graph_capture(torch_gpu):
+    """The entry point's first call in a process, made inside torch.cuda.graph capture (the
+    scratch address is looked up then), replayed three times against eager rg_gemm_fp32_ws."""
+    import os
+    import subprocess
+    import sys
+
+    worker = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_worker.py")
+    note("noalloc first call under capture (worker process)")
+    r = subprocess.run([sys.executable, worker], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True, timeout=300)
+    assert r.returncode == 0 and "noalloc capture ok" in r.stdout, r.stdout[-2000:]
+
+
 def test_noalloc_refuses_plans_beyond_the_scratch(torch_gpu):
     torch = torch_gpu
     M = N = K = 8192                     # digit panels alone: 2 * 8192 * 8192 * 3 B = 384 MiB
