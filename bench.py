@@ -295,7 +295,7 @@ def time_workload(torch, rg, A, B, n, steps, warmup, calibrate=False, steady=Fal
     return out
 
 
-def suite(torch, rg, reps=10, warmup=2):
+def suite(torch, rg, reps=10, warmup=2, out_path=None):
     """The 21 GEMMs of the reference's GPT-2 operation suite at 1024 tokens, S=3, with its
     input recipe (gpt2_ops_suite.cu:193-233, 463-483) and its timing method (median of `reps`
     event-timed calls after `warmup`, gpt2_ops_suite.cu:622-640), next to the times it recorded
@@ -307,6 +307,11 @@ def suite(torch, rg, reps=10, warmup=2):
     torch.backends.cuda.matmul.allow_tf32 = False
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     rows = []
+    # The reference suite's result-file format (gpt2_ops_suite.cu:591, 654-655), GEMM lines only,
+    # so compare_suite.sh can set these hashes beside the reference's recorded runs.
+    out_file = open(out_path, "w") if out_path else None
+    if out_file is not None:
+        out_file.write("# %s (this library) tokens=1024 S=3\n" % torch.cuda.get_device_name(0))
     for op in ops:
         M, N, K, ta, tb = op["M"], op["N"], op["K"], op["ta"], op["tb"]
         A = torch.from_numpy(normal_stream(M * K, op["seed"], scale=op["sa"])).cuda()
@@ -343,6 +348,16 @@ def suite(torch, rg, reps=10, warmup=2):
             return statistics.median(t)
 
         ms, base_ms = timed(run), timed(base)
+        if out_file is not None:
+            from bit_reproducible_training_amd.repro_gemm import _backend
+
+            C.view(torch.int32).fill_(-1)  # poisoned, then one more run, as the reference's suite
+            run()
+            hin = _backend.fnv1a64(B.cpu(), _backend.fnv1a64(A.cpu()))  # A then B
+            hout = _backend.fnv1a64(C.cpu())
+            out_file.write("OP\t%s\t%s\tin=%016x\tout=%016x\tms=%.4f\tbase_ms=%.4f\n" % (
+                op["name"], op["shape"], hin, hout, ms, base_ms))
+            out_file.flush()
         ref = op.get("reference_gpu_ms", {})
         best_ref = min((v["ms"] for v in ref.values()), default=None)
         rows.append({"op": op["name"], "shape": op["shape"], "ms": round(ms, 4),
@@ -352,6 +367,8 @@ def suite(torch, rg, reps=10, warmup=2):
                      "reference_best_gpu_ms": best_ref,
                      "speedup_vs_reference_best": round(best_ref / ms, 1) if best_ref else None})
         del A, B, C, ws
+    if out_file is not None:
+        out_file.close()
     total = sum(r["ms"] for r in rows)
     ref_total = sum(r["reference_best_gpu_ms"] for r in rows if r["reference_best_gpu_ms"])
     print(json.dumps({"mode": "suite", "tokens": 1024, "slices": 3, "ops": rows,
@@ -890,6 +907,9 @@ def main():
                     help="time the exact sum, convolutions, batched GEMM and Linear layer instead")
     ap.add_argument("--suite", action="store_true",
                     help="time the reference GPT-2 suite's 21 GEMMs (1024 tokens) instead")
+    ap.add_argument("--suite-out", default=None,
+                    help="with --suite: also write the reference suite's result file (OP lines "
+                         "with input and output hashes) to this path")
     ap.add_argument("--configs", action="store_true",
                     help="time every GEMM of BASELINE configurations 2, 3 and 5 instead")
     ap.add_argument("--sweep-plans", action="store_true",
@@ -913,7 +933,7 @@ def main():
     import bit_reproducible_training_amd as rg
 
     if args.suite:
-        suite(torch, rg)
+        suite(torch, rg, out_path=args.suite_out)
         return
     if args.configs:
         configs_mode(torch, rg)

@@ -278,8 +278,23 @@ void scan_finite(Tensor x, Tensor flag, int op_id) {
 
 }  // namespace
 
+// 64-bit FNV-1a over the raw bytes of a contiguous CPU tensor, continuing from h: the hash the
+// reference's tools print for inputs and outputs (repro_test_util.h:20-24,
+// gpt2_ops_suite.cu:80-88), so hashes printed here can be compared with theirs.
+uint64_t fnv1a64(const at::Tensor& t, uint64_t h) {
+    TORCH_CHECK(!t.is_cuda() && t.is_contiguous(), "fnv1a64: a contiguous CPU tensor");
+    const unsigned char* p = static_cast<const unsigned char*>(t.data_ptr());
+    const size_t n = (size_t)t.numel() * t.element_size();
+    for (size_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "Reproducible GEMM, exact sum and convolution on PyTorch tensors (MI355X or CPU)";
+    m.def("fnv1a64", &fnv1a64, py::arg("tensor"), py::arg("h") = 0xcbf29ce484222325ull);
     m.def("gemm", &gemm);
     m.def("gemm_ex", &gemm_ex);
     m.def("exact_sum", &exact_sum);

@@ -42,10 +42,11 @@ struct Config {
     bool trans_b = false;   // B stored N rows of K (op(B) = B^T) instead of K rows of N
 };
 
+// The planner's decision for one shape and Config on the current device.
 struct Plan {
-    Algo algo;               // resolved (never Auto)
-    int split_k;             // effective split count
-    size_t workspace_bytes;  // size needed by repro_gemm_fp32_ws
+    Algo algo;               // the algorithm that runs: TensorCore, Tiled or Reference
+    int split_k;             // K-parts the launch sums (the request, raised or clamped)
+    size_t workspace_bytes;  // the smallest workspace repro_gemm_fp32_ws accepts for it
 };
 
 inline rg_config to_c(const Config& c) {
@@ -61,8 +62,9 @@ inline rg_config to_c(const Config& c) {
     return r;
 }
 
-// hipErrorNotSupported: cfg.algo cannot run on the current device.
-// hipErrorInvalidValue: bad sizes/slices, or K too large for exact int64 at this S.
+// Errors: hipErrorNotSupported when the device is not gfx950 and cfg.algo needs the MFMA
+// contraction; hipErrorInvalidValue for sizes <= 0, S outside 1..3, a split_k <= 0, or a K
+// whose exact int64 sums could overflow at this S.
 inline hipError_t make_plan(int M, int N, int K, Config cfg, Plan* plan) {
     if (!plan) return hipErrorInvalidValue;
     rg_config c = to_c(cfg);
@@ -76,9 +78,10 @@ inline hipError_t make_plan(int M, int N, int K, Config cfg, Plan* plan) {
     return static_cast<hipError_t>(e);
 }
 
-// Asynchronous, allocation-free version for training loops. workspace must hold at
-// least plan.workspace_bytes. stage_events, if non-null, holds 4 events recorded on
-// `stream` before slicing, after slicing, after the contraction and after the final step.
+// The GEMM queued on `stream` with the caller's workspace (plan.workspace_bytes or more);
+// nothing is allocated and nothing waits, so a training loop calls this one. stage_events,
+// if non-null, are 4 events this call records on `stream`: before the slicing, after it,
+// after the contraction and after the final rounding.
 inline hipError_t repro_gemm_fp32_ws(const float* A, const float* B, float* C, int M, int N,
                                      int K, Config cfg, void* workspace,
                                      size_t workspace_bytes, hipStream_t stream = nullptr,
@@ -89,7 +92,8 @@ inline hipError_t repro_gemm_fp32_ws(const float* A, const float* B, float* C, i
         reinterpret_cast<void* const*>(stage_events)));
 }
 
-// Convenience version: allocates the workspace, runs, synchronizes, frees.
+// One-shot form: takes a workspace of its own with hipMalloc, runs repro_gemm_fp32_ws, waits
+// for the stream and releases the workspace (returning the first error met).
 inline hipError_t repro_gemm_fp32(const float* A, const float* B, float* C, int M, int N, int K,
                                   Config cfg = Config(), hipStream_t stream = nullptr) {
     rg_config c = to_c(cfg);
