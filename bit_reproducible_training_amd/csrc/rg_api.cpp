@@ -392,8 +392,8 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
         if (stage_events) (void)hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream);
     };
     if (L.small) {  // slicing, contraction and rounding in one kernel
-        if (opt.group_a > 0 || opt.group_b > 0 || opt.raw || opt.im2col_a || !A ||
-            L.K > SMALL_MAX_K)
+        if (opt.group_a > 0 || opt.group_b > 0 || opt.raw || opt.im2col_a || opt.nanrows_a ||
+            opt.nanrows_b || !A || L.K > SMALL_MAX_K)
             return hipErrorInvalidValue;
         record(0);
         record(1);
@@ -433,6 +433,7 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
         d.expo = expo;
         d.im2col = 0;
         std::memset(&d.g, 0, sizeof d.g);
+        d.nanrows = nullptr;
         slice_grid(d);
         d.spin_limit = slice_spin_limit();
         pslice_grid(d);
@@ -449,6 +450,8 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     }
     SliceDesc db = desc(B, L.N, L.Np, L.b_strided, addr.ldb, addr.stride_b, L.nch_b,
                         L.kch_b, pmb, qb, eb);
+    da.nanrows = opt.nanrows_a;
+    db.nanrows = opt.nanrows_b;
     const OutAddr out{addr.ldc, addr.stride_c};
 
     record(0);

@@ -77,12 +77,14 @@ size_t grid_for(size_t n) { return std::min<size_t>((n + THREADS - 1) / THREADS,
 // for the windows w0 .. w0 + count - 1. A block moves a tile of 64 windows x 64 positions
 // through LDS: it reads along the windows (consecutive windows of an output row are consecutive
 // pixels of x, so the loads coalesce) and writes along the positions (256 contiguous bytes of a
-// row of cols per wave).
+// row of cols per wave). nanw / nank (either may be null, both zeroed before): a NaN read for
+// window w at position k sets nanw[w] and nank[k] to 1, the rows whose maximum a NaN wins in the
+// forward pass (windows) and the weight gradient (positions).
 constexpr int IM2COL_TILE = 64;
 
 __global__ void __launch_bounds__(THREADS)
 im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uint32_t w0,
-              uint32_t count) {
+              uint32_t count, unsigned* __restrict__ nanw, unsigned* __restrict__ nank) {
     __shared__ float tile[IM2COL_TILE][IM2COL_TILE + 1];
     __shared__ long long koff[IM2COL_TILE];           // (c*H + ky)*W + kx of each position
     __shared__ int kys[IM2COL_TILE], kxs[IM2COL_TILE];
@@ -115,6 +117,10 @@ im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uin
             float v = 0.0f;
             if (live && kl < g.K - kt && (unsigned)y < (unsigned)g.H && (unsigned)xx < (unsigned)g.W)
                 v = x[base + koff[kl]];
+            if (__builtin_isnan(v)) {  // every writer stores the same 1
+                if (nanw) nanw[w] = 1u;
+                if (nank) nank[kt + kl] = 1u;
+            }
             tile[wl][kl] = v;
         }
     }
@@ -144,6 +150,13 @@ im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, Geom g, uin
             }
         }
     }
+}
+
+// p[0 .. n) = 0 (the NaN flags, before im2col_kernel sets some).
+__global__ void __launch_bounds__(THREADS) zero_flags_kernel(unsigned* __restrict__ p, long long n) {
+    for (long long i = (long long)blockIdx.x * THREADS + threadIdx.x; i < n;
+         i += (long long)gridDim.x * THREADS)
+        p[i] = 0u;
 }
 
 // dst[b][c][r] = src[b][r][c] for `batch` matrices of rows x cols, through a 32 x 33 LDS tile
@@ -404,13 +417,14 @@ fwd_direct_kernel(const float* __restrict__ x, const float* __restrict__ w, floa
         const int p = w0 + t;
         const int oy = (int)fdiv((uint32_t)p, g.dOW), ox = p - oy * g.OW;
         const float* base = patch + (oy - oy_lo) * g.SY * PW + ox * g.SX;
-        float m = 0.0f;
+        // Magnitude bits: a NaN in the window wins, and the window takes exponent 0.
+        unsigned mb = 0;
         for (int c = 0; c < g.C; ++c)
             for (int ky = 0; ky < g.KH; ++ky) {
                 const float* row = base + (c * rows + ky) * PW;
-                for (int kx = 0; kx < g.KW; ++kx) m = fmaxf(m, fabsf(row[kx]));
+                for (int kx = 0; kx < g.KW; ++kx) mb = max(mb, __float_as_uint(row[kx]) & 0x7FFFFFFFu);
             }
-        sew[t] = repro_gemm::scale_exponent(m);
+        sew[t] = repro_gemm::scale_exponent(__uint_as_float(mb));
     }
     __syncthreads();
     const int wi = t % nw, gi = t / nw;
@@ -683,6 +697,8 @@ struct ConvPlan {
     bool implicit;   // forward GEMM reads the im2col matrix through Im2col (no cols buffer)
     Layout L;        // the GEMM (GEMM algorithm only)
     size_t buf0, buf1, gemm, total;
+    size_t flags;    // NaN flags of the packed cols' windows (forward) or positions (weight
+    long long nflags;  // gradient), one per padded row of that GEMM operand; 0 if none
 };
 
 int conv_plan(Kind kind, const rg_conv_shape* s, int S, int algo, ConvPlan* P) {
@@ -720,12 +736,14 @@ int conv_plan(Kind kind, const rg_conv_shape* s, int S, int algo, ConvPlan* P) {
             p.implicit = e == hipSuccess && p.L.Kp <= ONEPASS_MAX_K;
             b0 = p.implicit ? 0 : (size_t)W * g.K * sizeof(float);   // cols
             b1 = (size_t)W * g.F * sizeof(float);                     // Y rows
+            if (e == hipSuccess && !p.implicit) p.nflags = p.L.Mp;    // windows
             break;
         case Kind::GradWeight:    // dW[F][K] = (dY rows[W][F])^T * cols[W][K]
             cfg.trans_a = 1;
             e = layout_for_current_device(g.F, g.K, W, &cfg, &p.L, conv_extras(false));
             b0 = (size_t)W * g.F * sizeof(float);   // dY rows
             b1 = (size_t)W * g.K * sizeof(float);   // cols
+            if (e == hipSuccess) p.nflags = p.L.Np;  // positions
             break;
         case Kind::GradInput:     // T^T[K][W] = weight^T[K][F] * (dY rows[W][F])^T, exact int64
             // Transposed, so that the pixels of one row read neighbouring windows of one
@@ -739,23 +757,34 @@ int conv_plan(Kind kind, const rg_conv_shape* s, int S, int algo, ConvPlan* P) {
     if (e != hipSuccess) return e;
     p.buf0 = 0;
     p.buf1 = align_up(b0);
-    p.gemm = p.buf1 + align_up(b1);
+    p.flags = p.buf1 + align_up(b1);
+    p.gemm = p.flags + align_up((size_t)p.nflags * sizeof(unsigned));
     p.total = p.gemm + p.L.total;
     *P = p;
     return hipSuccess;
 }
 
+// Zeroes the plan's NaN flags (a kernel rather than a memset node, so that a captured graph
+// replays it correctly).
+unsigned* zero_flags(const ConvPlan& p, char* base, hipStream_t stream) {
+    unsigned* f = reinterpret_cast<unsigned*>(base + p.flags);
+    hipLaunchKernelGGL(zero_flags_kernel, dim3((unsigned)grid_for((size_t)p.nflags)), dim3(THREADS),
+                       0, stream, f, (long long)p.nflags);
+    return f;
+}
+
 // cols for every window. Consecutive blocks take the position tiles of one window tile (grid
 // x), so a row of cols is completed, and its patch of x read, by neighbouring blocks; launches
 // of at most 65535 window tiles (grid y).
-void launch_im2col(const float* x, float* cols, const Geom& g, hipStream_t stream) {
+void launch_im2col(const float* x, float* cols, const Geom& g, unsigned* nanw, unsigned* nank,
+                   hipStream_t stream) {
     const long long per = 65535LL * IM2COL_TILE;
     const unsigned ktiles = (unsigned)((g.K + IM2COL_TILE - 1) / IM2COL_TILE);
     for (long long w0 = 0; w0 < g.windows; w0 += per) {
         const long long nw = std::min<long long>(per, g.windows - w0);
         const unsigned wtiles = (unsigned)((nw + IM2COL_TILE - 1) / IM2COL_TILE);
         hipLaunchKernelGGL(im2col_kernel, dim3(ktiles, wtiles), dim3(THREADS), 0, stream, x, cols,
-                           g, (uint32_t)w0, (uint32_t)nw);
+                           g, (uint32_t)w0, (uint32_t)nw, nanw, nank);
     }
 }
 
@@ -827,9 +856,13 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
                 e = gemm_launch(nullptr, b, yrows, p.L, gws, stream, nullptr, opt,
                                 dense_addressing(p.L));
             } else {
+                // Windows holding a NaN take exponent 0 (their maximum compares raw bits).
                 float* cols = reinterpret_cast<float*>(base + p.buf0);
-                launch_im2col(a, cols, g, stream);
-                e = gemm_launch(cols, b, yrows, p.L, gws, stream, nullptr, GemmOptions(),
+                GemmOptions opt;
+                unsigned* nanw = zero_flags(p, base, stream);
+                opt.nanrows_a = nanw;
+                launch_im2col(a, cols, g, nanw, nullptr, stream);
+                e = gemm_launch(cols, b, yrows, p.L, gws, stream, nullptr, opt,
                                 dense_addressing(p.L));
             }
             if (e != hipSuccess) return e;
@@ -840,8 +873,12 @@ int run_pass(Kind kind, const float* a, const float* b, float* out, const rg_con
             float* dyrows = reinterpret_cast<float*>(base + p.buf0);
             float* cols = reinterpret_cast<float*>(base + p.buf1);
             launch_nfp_rows(a, dyrows, g, true, stream);
-            launch_im2col(b, cols, g, stream);
-            e = gemm_launch(dyrows, cols, out, p.L, gws, stream, nullptr, GemmOptions(),
+            // Positions holding a NaN in some window take exponent 0 (raw-bit maxima).
+            GemmOptions opt;
+            unsigned* nank = zero_flags(p, base, stream);
+            opt.nanrows_b = nank;
+            launch_im2col(b, cols, g, nullptr, nank, stream);
+            e = gemm_launch(dyrows, cols, out, p.L, gws, stream, nullptr, opt,
                             dense_addressing(p.L));
             if (e != hipSuccess) return e;
             break;

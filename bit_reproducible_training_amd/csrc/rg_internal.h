@@ -210,6 +210,10 @@ struct SliceDesc {
     int ps_parts;
     int spin_limit;
     long long ps_blocks;
+    // Null, or one flag per stacked row (batch * Rp): a row whose flag is non-zero takes
+    // exponent 0, the exponent of a maximum that a NaN wins (the convolution's window and
+    // position maxima; the maxima computed here skip NaN).
+    const unsigned* nanrows;
 };
 
 // Bit pattern of a partial-maximum slot not yet written by this call (a NaN; no maximum of
@@ -291,6 +295,9 @@ struct GemmOptions {
     // pass on the implicit im2col matrix); needs the one-pass route (padded K <= ONEPASS_MAX_K,
     // no group scales, one item).
     const Im2col* im2col_a = nullptr;
+    // Row flags of op(A) and of op(B)^T (SliceDesc::nanrows), padded to Mp and Np rows.
+    const unsigned* nanrows_a = nullptr;
+    const unsigned* nanrows_b = nullptr;
 };
 
 // Layout for the current device (queried once per device and cached).

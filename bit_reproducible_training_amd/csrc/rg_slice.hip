@@ -28,6 +28,19 @@ __device__ __forceinline__ float max4(float4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
+// Largest magnitude bits of v: for non-NaN values the bits of max4(v); a NaN wins.
+__device__ __forceinline__ unsigned max4_bits(float4 v) {
+    const unsigned a = __float_as_uint(v.x) & 0x7FFFFFFFu, b = __float_as_uint(v.y) & 0x7FFFFFFFu;
+    const unsigned c = __float_as_uint(v.z) & 0x7FFFFFFFu, e = __float_as_uint(v.w) & 0x7FFFFFFFu;
+    return max(max(a, b), max(c, e));
+}
+
+// Exponent of stacked row q from its maximum m (which skips NaN), or 0 where d.nanrows flags
+// the row.
+__device__ __forceinline__ int row_exponent(const SliceDesc& d, size_t q, float m) {
+    return d.nanrows && d.nanrows[q] ? 0 : scale_exponent(m);
+}
+
 // Row access, element (r, k) of item b at src[b*bstride + r*ld + k]: wavefront w of the
 // operand handles row w / nch of all items' rows (item-major), chunk w % nch.
 // (row, chunk) pairs per wavefront in the row-access maxima: a lane per pair for short
@@ -438,7 +451,7 @@ __device__ void split_operand(const SliceDesc& d, long long blk) {
         float m = smax[0][t];
 #pragma unroll
         for (int i = 1; i < 8; ++i) m = fmaxf(m, smax[i][t]);
-        const int se = scale_exponent(m);  // rows >= R have m == 0, so se == 0
+        const int se = row_exponent(d, rp * PANEL_ROWS + t, m);  // rows >= R: m == 0, se == 0
         sse[t] = se;
         if (kg == 0) d.expo[rp * PANEL_ROWS + t] = se;
     }
@@ -553,17 +566,21 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
             x0 = ox * g.SX - g.PX;
             xn = g.x + (size_t)n * g.C * g.H * g.W;
         }
-        float m = 0.0f;
 #pragma unroll
         for (int i = 0; i < NF4; ++i) {
             const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
             v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             if (row < d.R && k < d.K) v[i] = im2col_values(g, xn, y0, x0, k, d.K);
         }
+        // A window's maximum compares magnitude bits, so a NaN in the window wins and the
+        // window takes exponent 0 (repro_conv_math.cuh:73-86); the reduction across the
+        // wavefronts below keeps it (bits).
+        unsigned mb = 0;
 #pragma unroll
-        for (int i = 0; i < NF4; ++i) m = fmaxf(m, max4(v[i]));
+        for (int i = 0; i < NF4; ++i) mb = max(mb, max4_bits(v[i]));
 #pragma unroll
-        for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        for (int off = 1; off < 8; off <<= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, off, 64));
+        const float m = __uint_as_float(mb);
         if (WS) wmax = m;  // lanes 8j..8j+7 all hold row j's maximum
         else if ((lane & 7) == 0) smax[w][lane >> 3] = m;
     } else if (!d.strided) {
@@ -644,15 +661,19 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
     }
     int lane_se = 0;  // WS: exponent of this lane's row (row or column lane / 8 of the strip)
     if (WS) {
-        lane_se = scale_exponent(wmax);  // rows >= R have a zero maximum, so exponent 0
+        // rows >= R have a zero maximum, so exponent 0
+        lane_se = row_exponent(d, (size_t)item * d.Rp + r0 + (lane >> 3), wmax);
         if ((lane & 7) == 0) d.expo[(size_t)item * d.Rp + r0 + (lane >> 3)] = lane_se;
     } else {
         __syncthreads();
         if (threadIdx.x < 8) {
-            float m = smax[0][threadIdx.x];
+            // The partial maxima are non-negative, so their bits order like them (a gathered
+            // window's NaN wins).
+            unsigned mb = __float_as_uint(smax[0][threadIdx.x]);
 #pragma unroll
-            for (int i = 1; i < 8; ++i) m = fmaxf(m, smax[i][threadIdx.x]);
-            const int se = scale_exponent(m);  // rows >= R have m == 0, so se == 0
+            for (int i = 1; i < 8; ++i) mb = max(mb, __float_as_uint(smax[i][threadIdx.x]));
+            // rows >= R have a zero maximum, so exponent 0
+            const int se = row_exponent(d, (size_t)item * d.Rp + r0 + threadIdx.x, __uint_as_float(mb));
             sse[threadIdx.x] = se;
             d.expo[(size_t)item * d.Rp + r0 + threadIdx.x] = se;
         }
@@ -962,7 +983,8 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
         __syncthreads();
     }
     if (t < 32) {
-        const int se = scale_exponent(sfin[t]);  // rows >= R have a zero maximum, so se == 0
+        // rows >= R have a zero maximum, so se == 0
+        const int se = row_exponent(d, rp * PANEL_ROWS + t, sfin[t]);
         sse[t] = se;
         if (part == 0) d.expo[rp * PANEL_ROWS + t] = se;
     }
@@ -1052,7 +1074,8 @@ __device__ void pslice_rows(const SliceDesc& d, long long blk) {
         __syncthreads();
     }
     if (t < 8) {
-        const int se = scale_exponent(sfin[t]);  // rows >= R have a zero maximum, so se == 0
+        // rows >= R have a zero maximum, so se == 0
+        const int se = row_exponent(d, (size_t)item * d.Rp + r0 + t, sfin[t]);
         sse[t] = se;
         if (part == 0) d.expo[(size_t)item * d.Rp + r0 + t] = se;
     }

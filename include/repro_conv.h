@@ -55,7 +55,9 @@ int rg_conv2d_grad_input_workspace(const rg_conv_shape* g, int S, size_t* bytes)
 /* Replace repro_conv2d_ws / repro_conv2d_grad_weight_ws / repro_conv2d_grad_input_ws
  * (repro_conv_cuda/repro_conv.cuh:26-31, repro_conv.cu:189-241). Asynchronous on `stream`,
  * allocation-free. Errors as the workspace functions, plus 1 for null tensors or a workspace
- * that is null or too small, and any launch error. Inputs must be finite. */
+ * that is null or too small, and any launch error. Inputs are meant to be finite; a NaN or an
+ * infinity gives the bits of the reference's CPU convolution (a NaN wins a window's or a
+ * position's maximum, which then takes exponent 0). */
 int rg_conv2d_ws(const float* x, const float* weight, float* out, const rg_conv_shape* g, int S,
                  void* workspace, size_t workspace_bytes, void* stream);
 int rg_conv2d_grad_weight_ws(const float* dy, const float* x, float* dw, const rg_conv_shape* g,

@@ -17,7 +17,8 @@
 // share one scale per image of dY and one for all weights.
 //
 // Each entry point throws std::invalid_argument for a null pointer or a shape the GPU entry
-// points reject (cpu_shape_valid). Inputs must be finite.
+// points reject (cpu_shape_valid). Inputs are meant to be finite; a NaN or an infinity still
+// gives the reference's CPU bits (see conv_detail::raw_magnitude_bits).
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -55,9 +56,12 @@ inline void require(bool ok, const char* what) {
     if (!ok) throw std::invalid_argument(what);
 }
 
-// Ordering key of |v| for the maxima: its bits, with NaN skipped as in the GEMM (the
-// reference's convolution compares raw magnitude bits, so a NaN wins there; skipping it keeps
-// the convolution equal to the GEMM on its im2col matrix for every input, and equal to the GPU).
+// The reference takes two kinds of maxima. The window maxima of the forward pass and the
+// position maxima of the weight gradient compare the raw bits of |v|, so a NaN (bits above
+// +inf) wins and its scale exponent is 0 (repro_conv_math.cuh:73-86, 121-130). The filter,
+// dY and weight maxima use std::max on floats, which skips a NaN (repro_conv_cpu.h:29,48,77,82).
+// For finite inputs both give the same maximum.
+inline uint32_t raw_magnitude_bits(float v) { return repro_gemm::float_to_bits(v) & 0x7FFFFFFFu; }
 inline uint32_t magnitude_bits(float v) { return repro_gemm::magnitude_key(v); }
 
 // Values of window w (= (n, oy, ox)) at every position k, zero in the padding.
@@ -92,7 +96,7 @@ inline void cpu_conv2d(const float* x, const float* w, float* out, const ConvSha
         std::vector<int32_t> q(K);
         conv_detail::gather_window(x, g, win, vals.data());
         uint32_t top = 0;
-        for (int k = 0; k < K; ++k) top = std::max(top, conv_detail::magnitude_bits(vals[k]));
+        for (int k = 0; k < K; ++k) top = std::max(top, conv_detail::raw_magnitude_bits(vals[k]));
         const int e = scale_exponent(bits_to_float(top));
         for (int k = 0; k < K; ++k) q[k] = fixed_point(vals[k], e, S);
         const int n = win / P, p = win % P;
@@ -138,7 +142,7 @@ inline void cpu_conv2d_grad_weight(const float* dy, const float* x, float* dw, c
             const float v = (y >= 0 && y < g.H && xx >= 0 && xx < g.W)
                                 ? x[(((size_t)n * g.C + c) * g.H + y) * g.W + xx] : 0.0f;
             col[win] = v;
-            top = std::max(top, conv_detail::magnitude_bits(v));
+            top = std::max(top, conv_detail::raw_magnitude_bits(v));
         }
         const int e = scale_exponent(bits_to_float(top));
         std::vector<int32_t> q(Wn);

@@ -660,6 +660,15 @@ static float conv_window_value(const float* x, const oracle_conv_shape* g, int n
 static int conv_oh(const oracle_conv_shape* g) { return (g->H + 2 * g->PY - g->KH) / g->SY + 1; }
 static int conv_ow(const oracle_conv_shape* g) { return (g->W + 2 * g->PX - g->KW) / g->SX + 1; }
 
+/* Largest magnitude bit pattern of m and x: the window and position maxima of the reference's
+ * convolution compare raw magnitude bits (repro_conv_math.cuh:73-86, 121-130), so a NaN (whose
+ * bits exceed +inf's) wins them and its window or position gets exponent 0; the filter and dY
+ * maxima use std::max on values, which skips a NaN (repro_conv_cpu.h:29, 48, 77, 82). */
+static uint32_t conv_bits_max(uint32_t m, float x) {
+    uint32_t a = f2u(x) & 0x7FFFFFFFu;
+    return a > m ? a : m;
+}
+
 /* Forward (repro_conv_cpu.h:23-38, repro_conv_math.cuh:68-99): weights quantised per filter,
  * each window per window, Y[n][f][oy][ox] = round(sum_k X * W, e_window + e_filter + e0). */
 void oracle_conv2d(const float* x, const float* w, float* out, const oracle_conv_shape* g, int S) {
@@ -677,13 +686,13 @@ void oracle_conv2d(const float* x, const float* w, float* out, const oracle_conv
     for (int n = 0; n < g->N; ++n)
         for (int oy = 0; oy < oh; ++oy)
             for (int ox = 0; ox < ow; ++ox) {
-                float m = 0.0f;
+                uint32_t mb = 0;
                 for (int k = 0; k < K; ++k) {
                     int c = k / (g->KH * g->KW), r = k % (g->KH * g->KW);
                     v[k] = conv_window_value(x, g, n, oy, ox, c, r / g->KW, r % g->KW);
-                    m = fmaxf(m, fabsf(v[k]));
+                    mb = conv_bits_max(mb, v[k]);
                 }
-                int e = oracle_scale_exponent(m);
+                int e = oracle_scale_exponent(u2f(mb));
                 for (int k = 0; k < K; ++k) q[k] = oracle_fixed_point(v[k], e, S);
                 for (int f = 0; f < g->F; ++f) {
                     int64_t t = 0;
@@ -715,11 +724,11 @@ void oracle_conv2d_grad_weight(const float* dy, const float* x, float* dw,
     for (size_t i = 0; i < outn; ++i) D[i] = oracle_fixed_point(dy[i], eF[(i / P) % g->F], S);
     for (int k = 0; k < K; ++k) {
         int c = k / (g->KH * g->KW), r = k % (g->KH * g->KW), ky = r / g->KW, kx = r % g->KW;
-        float m = 0.0f;
+        uint32_t mb = 0;
         for (int n = 0; n < g->N; ++n)
             for (size_t p = 0; p < P; ++p)
-                m = fmaxf(m, fabsf(conv_window_value(x, g, n, (int)(p / ow), (int)(p % ow), c, ky, kx)));
-        int eX = oracle_scale_exponent(m);
+                mb = conv_bits_max(mb, conv_window_value(x, g, n, (int)(p / ow), (int)(p % ow), c, ky, kx));
+        int eX = oracle_scale_exponent(u2f(mb));
         for (int n = 0; n < g->N; ++n)
             for (size_t p = 0; p < P; ++p)
                 X[(size_t)n * P + p] = oracle_fixed_point(

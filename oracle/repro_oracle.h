@@ -38,7 +38,9 @@
  *                          gradient against oracle_cpu_gemm on the im2col matrix (an
  *                          independent path); the input gradient against brute force with
  *                          Python integers on small shapes; all three against oracle/_ref
- *                          (the reference's repro_conv_cpu.h compiled here).
+ *                          (the reference's repro_conv_cpu.h compiled here), on finite
+ *                          inputs and on inputs with NaN and infinities; a hand case
+ *                          whose window holds a NaN (exponent 0).
  */
 #ifndef REPRO_ORACLE_H
 #define REPRO_ORACLE_H

@@ -9,7 +9,7 @@ import pytest
 import bit_reproducible_training_amd as rg
 from gpu_util import note, run, to_dev
 from oracle import oracle as O
-from test_nonfinite import TRANSPOSES, nonfinite_inputs
+from test_nonfinite import TRANSPOSES, conv_oracle, nonfinite_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -54,8 +54,9 @@ def test_nonfinite_batched_matches_oracle(torch_gpu):
 @pytest.mark.parametrize("S", [1, 3])
 def test_nonfinite_convolution_matches_oracle(torch_gpu, S):
     """Convolutions with NaN and infinities in x, w and dY, by the direct kernels, by the GEMM
-    pipeline and by the automatic choice: the oracle's bits (maxima skip NaN, a non-finite value
-    counts as -127 * 2^(7(S-1)))."""
+    pipeline and by the automatic choice: the oracle's bits (a NaN wins the window and position
+    maxima and is skipped by the filter, dY and weight maxima; a non-finite value counts as
+    -127 * 2^(7(S-1)))."""
     from test_gpu_conv import RC, _run_algo
     from test_nonfinite import CONV_SHAPE, conv_nonfinite_inputs, conv_oracle
 
@@ -69,6 +70,56 @@ def test_nonfinite_convolution_matches_oracle(torch_gpu, S):
                 note("nonfinite conv", kind, shape, "S=%d algo=%d" % (S, algo))
                 got = _run_algo(torch, kind, a.ravel(), b.ravel(), shape, S, algo)
                 assert np.array_equal(got.view(np.uint32).ravel(), want), (kind, shape, algo)
+
+
+# Shapes whose window maxima (forward) and position maxima (weight gradient) go through each
+# route: forward gathered in one pass with K = 288 (one wavefront per strip past K = 256), with
+# K = 27 and 9 (wave strips), packed with K = 4608 (one read in two parts per 8-row strip) and
+# K = 147456 (two passes: 36 parts would be too many); weight gradient over 200 windows (one
+# pass), 5000 (one read in parts along the windows) and 40000 (two passes).
+NAN_ROUTE_SHAPES = [
+    (2, 32, 10, 10, 8, 3, 3, 1, 1, 1, 1), (1, 512, 6, 6, 4, 3, 3, 1, 1, 1, 1),
+    (1, 16384, 3, 3, 2, 3, 3, 1, 1, 0, 0), (2, 2, 50, 50, 4, 3, 3, 1, 1, 1, 1),
+    (4, 1, 100, 100, 2, 3, 3, 1, 1, 1, 1),
+]
+DIRECT_FORWARD = {0, 3, 4}  # indices of the shapes the direct forward kernel takes
+
+
+def _plant_nonfinite(rng, t, count):
+    """count NaN and one +inf at random places of t (in place)."""
+    flat = t.reshape(-1)
+    idx = rng.choice(flat.size, count + 1, replace=False)
+    flat[idx[:-1]] = np.nan
+    flat[idx[-1]] = np.inf
+
+
+@pytest.mark.parametrize("S", [1, 3])
+@pytest.mark.parametrize("si", range(len(NAN_ROUTE_SHAPES)))
+def test_nonfinite_convolution_routes_match_oracle(torch_gpu, S, si):
+    """A NaN in x wins the maxima of the windows (forward) and positions (weight gradient) it
+    falls in, which then take exponent 0, on every slicing route of both passes, as in the
+    reference's convolution (repro_conv_math.cuh:73-86, 121-130); the oracle's convolution is
+    pinned to the reference's CPU path on such inputs by the CPU tests."""
+    from test_gpu_conv import RC, _run_algo
+
+    torch = torch_gpu
+    shape = NAN_ROUTE_SHAPES[si]
+    N, C, H, W, F, KH, KW = shape[:7]
+    OH, OW = O.conv_out_hw(shape)
+    rng = np.random.default_rng(70 + 7 * S + si)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = rng.standard_normal((F, C, KH, KW)).astype(np.float32)
+    dy = rng.standard_normal((N, F, OH, OW)).astype(np.float32)
+    _plant_nonfinite(rng, x, 3)
+    for kind, a, b in (("fwd", x, w), ("dW", dy, x)):
+        want = conv_oracle(kind, x, w, dy, shape, S).view(np.uint32).ravel()
+        algos = [RC.ALGO_GEMM, RC.ALGO_AUTO]
+        if kind == "fwd" and si in DIRECT_FORWARD:
+            algos.append(RC.ALGO_DIRECT)
+        for algo in algos:
+            note("nonfinite conv route", kind, shape, "S=%d algo=%d" % (S, algo))
+            got = _run_algo(torch, kind, a.ravel(), b.ravel(), shape, S, algo)
+            assert np.array_equal(got.view(np.uint32).ravel(), want), (kind, shape, algo)
 
 
 @pytest.mark.parametrize("chunk", range(2))

@@ -125,22 +125,41 @@ def _bits(a):
 
 @pytest.mark.parametrize("S", [1, 3])
 def test_conv_cpu_path_matches_oracle_on_nonfinite_inputs(S):
-    """The convolution's maxima skip NaN as the GEMM's do (the reference's convolution lets a
-    NaN win its maxima, so it gives other bits where a NaN is present); infinities and the
-    -127 * 2^(7(S-1)) of a non-finite value are as in the GEMM."""
+    """The window maxima (forward) and position maxima (weight gradient) compare magnitude
+    bits, so a NaN wins them and that window or position takes exponent 0; the filter, dY and
+    weight maxima skip NaN; infinities and the -127 * 2^(7(S-1)) of a non-finite value are as
+    in the GEMM."""
     x, w, dy = conv_nonfinite_inputs(CONV_SHAPE, 20 + S)
     for kind in ("fwd", "dW", "dX"):
         assert np.array_equal(_bits(_conv_cpu(kind, x, w, dy, CONV_SHAPE, S)),
                               _bits(conv_oracle(kind, x, w, dy, CONV_SHAPE, S))), kind
 
 
-@pytest.mark.parametrize("S", [1, 3])
-def test_conv_oracle_matches_reference_with_infinities(S):
-    """With infinities and no NaN both kinds of maxima agree, so the oracle's convolution must
-    give the reference convolution's own bits (oracle/_ref)."""
+@pytest.mark.parametrize("nan", [False, True])
+@pytest.mark.parametrize("S", [1, 2, 3])
+def test_conv_oracle_matches_reference_on_nonfinite_inputs(S, nan):
+    """The oracle's convolution gives the reference convolution's own bits (oracle/_ref) with
+    infinities, and with NaN in x, the weights and dY."""
     if O.ref is None:
         pytest.skip("oracle/_ref (the reference's CPU path) is not built here")
-    x, w, dy = conv_nonfinite_inputs(CONV_SHAPE, 30 + S, nan=False)
-    for kind, a, b in (("fwd", x, w), ("dW", dy, x), ("dX", dy, w)):
-        assert np.array_equal(_bits(O.ref_conv(kind, a, b, CONV_SHAPE, S)),
-                              _bits(conv_oracle(kind, x, w, dy, CONV_SHAPE, S))), kind
+    for seed in range(3):
+        x, w, dy = conv_nonfinite_inputs(CONV_SHAPE, 30 + 4 * S + seed, nan=nan)
+        for kind, a, b in (("fwd", x, w), ("dW", dy, x), ("dX", dy, w)):
+            assert np.array_equal(_bits(O.ref_conv(kind, a, b, CONV_SHAPE, S)),
+                                  _bits(conv_oracle(kind, x, w, dy, CONV_SHAPE, S))), (kind, seed)
+
+
+def test_conv_oracle_nan_window_takes_exponent_zero():
+    """Hand case: 1x1 image row [NaN, 2, 1, 0.5] (N=1, C=1, H=1, W=4), one 1x2 filter [1, 1],
+    stride 1, no padding, S=1. Windows [NaN, 2] and [2, 1], [1, 0.5]. The first window's maximum
+    is the NaN, exponent 0: X = [-127, 2 * 2^0 -> 2], so y0 = round((-127 + 2) * 2^(e_f)) with
+    the filter's e_f = -6 (1/127 <= 2^-6), Wq = [64, 64], sum = -125 * 64 = -8000, times
+    2^(0 - 6) = -125. The second window: max 2, e = -5, X = [64, 32], sum = 96 * 64 = 6144,
+    times 2^(-11) = 3.0. The third: max 1, e = -6, X = [64, 32], sum 6144 * 2^-12 = 1.5.
+    Skipping the NaN instead would give the first window e = -5 and y0 = (-127 + 64) * 64 * 2^-11
+    = -1.96875."""
+    x = np.array([np.nan, 2.0, 1.0, 0.5], np.float32).reshape(1, 1, 1, 4)
+    w = np.ones((1, 1, 1, 2), np.float32)
+    shape = (1, 1, 1, 4, 1, 1, 2, 1, 1, 0, 0)
+    y = np.asarray(O.conv2d(x, w, shape, 1), np.float32).ravel()
+    assert y.tolist() == [-125.0, 3.0, 1.5]
