@@ -36,8 +36,9 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 # The steady-state side measurement of the headline GEMM: GEMMs run first, then GEMMs timed.
 STEADY_WARM = 200
 STEADY_STEPS = 50
-# HBM bytes per GEMM at 4096^3 S=3 (fetch + write) of the contraction launch and of the two
-# slicing launches, from rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by the same counters on a
+# HBM bytes per GEMM at 4096^3 S=3 (fetch + write) of the contraction launch and of the
+# slicing launches (the slot marking and the one-read slicing), from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE scaled by the same counters on a
 # 256 MiB device copy (profiles/contract_mfma_4096cube_traffic.md), each measured on the sources
 # whose SHA-256 (sources_digest) is given: the kernel file and rg_internal.h, which holds the
 # block order and the rounding helpers. A counter value cannot be read from inside this process,
@@ -45,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "314465f63784c10e2681b472e1c4d752b2b2a1f862aa38448049b7802d7a17e5"),
-    "slicing": (303693824, ("rg_slice.hip", "rg_internal.h"),
-                "680058bf83c90e0c583fe452b8d529c60ad4c98c3805b1640d73a2378856ed6e"),
+                 "70c5caaaecae614686e05fab758834f13b42f67f24904688ff51d5482bc88f82"),
+    "slicing": (235581338, ("rg_slice.hip", "rg_internal.h"),
+                "bbfed543b8d3b8c45ce1a3b7c0725e982ea4514b00011432919f77b153ba2564"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
@@ -275,12 +276,7 @@ def time_workload(torch, rg, A, B, n, steps, warmup, calibrate=False, steady=Fal
         torch.cuda.synchronize()
         steady_ms = (time.perf_counter() - t0) * 1e3 / STEADY_STEPS
     if calibrate:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibration_copies(torch)
     out = {
         "ms_per_step": wall * 1e3 / steps,
         "slice_ms": statistics.mean(e[0].elapsed_time(e[1]) for e in evs),
@@ -653,7 +649,19 @@ def _graph_ms(torch, step, reps=20):
     return e0.elapsed_time(e1) / (5 * reps)
 
 
-def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
+def calibration_copies(torch):
+    """Three device-to-device copies of 256 MiB: a plain copy kernel of known size, whose
+    rocprofv3 FETCH_SIZE / WRITE_SIZE readings scale those of the library's kernels."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0, only=None, warm_gpu_ms=400.0,
+                 calibrate=False):
     """One JSON line: every GEMM of BASELINE configurations 1, 2, 3 and 5 timed on the GPU in
     steady state: back-to-back GEMMs for about `warm_ms` of GPU time (past the GPU's
     power-management transient after a change of load), then HIP events around about `timed_ms`
@@ -661,12 +669,17 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
     effective FP32 TFLOP/s, the stage times (median of
     5 runs with stage events: slicing, contraction, final rounding), the contraction's share of the
     dense int8 MFMA peak, the plan, and whether the runs gave identical bits. GEMMs of less than
-    0.1 ms also get `graph_ms`, the GPU time per GEMM without the host's launch cost."""
+    0.1 ms also get `graph_ms`, the GPU time per GEMM without the host's launch cost.
+    `only`: names of the cases to run (all if None); warm_gpu_ms = 0 skips bringing the GPU out
+    of idle (for profiler runs, where the timings are not the point)."""
+    if calibrate:
+        calibration_copies(torch)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2024)
     sp = torch.cuda.current_stream().cuda_stream
     rows = []
-    warm_gpu(torch, rg)
+    if warm_gpu_ms > 0:
+        warm_gpu(torch, rg, warm_gpu_ms)
     # What two stage events recorded back to back measure with no launch between them: taken off
     # the stage times before the HBM rates below are computed.
     fe = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
@@ -677,9 +690,15 @@ def configs_mode(torch, rg, warm_ms=40.0, timed_ms=20.0):
         torch.cuda.synchronize()
         floor.append(fe[0].elapsed_time(fe[1]))
     event_floor_ms = statistics.median(floor)
-    for name, M, N, K, ta, tb, S, sa, sb in _config_cases():
-        if name == "c3.qkv.fwd":  # after the tiny LeNet GEMMs, which leave the GPU almost idle
-            warm_gpu(torch, rg)
+    cases = _config_cases()
+    if only:
+        unknown = set(only) - {c[0] for c in cases}
+        if unknown:
+            raise SystemExit("bench.py --case: unknown case(s) %s" % ", ".join(sorted(unknown)))
+        cases = [c for c in cases if c[0] in only]
+    for name, M, N, K, ta, tb, S, sa, sb in cases:
+        if name == "c3.qkv.fwd" and warm_gpu_ms > 0:  # after the tiny LeNet GEMMs, which leave the GPU almost idle
+            warm_gpu(torch, rg, warm_gpu_ms)
         def draw(n, scale):
             if scale < 0:  # U(-|scale|, |scale|)
                 return (torch.rand(n, device="cuda", generator=gen) * 2 - 1) * -scale
@@ -911,7 +930,13 @@ def main():
                     help="with --suite: also write the reference suite's result file (OP lines "
                          "with input and output hashes) to this path")
     ap.add_argument("--configs", action="store_true",
-                    help="time every GEMM of BASELINE configurations 2, 3 and 5 instead")
+                    help="time every GEMM of BASELINE configurations 1, 2, 3 and 5 instead")
+    ap.add_argument("--case", default=None,
+                    help="with --configs: comma-separated case names to run (e.g. "
+                         "c5.tall_skinny,c3.attn_proj.dW)")
+    ap.add_argument("--warm-ms", type=float, default=400.0,
+                    help="with --configs: ms of 4096^3 GEMMs that bring the GPU out of idle "
+                         "first (0 skips them, for profiler runs)")
     ap.add_argument("--sweep-plans", action="store_true",
                     help="time every block tile x split on the planner's fitting shapes instead")
     ap.add_argument("--accuracy", action="store_true",
@@ -936,7 +961,8 @@ def main():
         suite(torch, rg, out_path=args.suite_out)
         return
     if args.configs:
-        configs_mode(torch, rg)
+        configs_mode(torch, rg, only=args.case.split(",") if args.case else None,
+                     warm_gpu_ms=args.warm_ms, calibrate=args.calibrate)
         return
     if args.accuracy:
         accuracy_mode(torch, rg)
@@ -1021,9 +1047,9 @@ def main():
                                "launch per step; achieved = ops / HIP-event duration"},
         # The slicing stage against the HBM roofline: algorithmic bytes = fp32 inputs read once
         # (4(MK + KN)) + S digit planes written (S(MK + NK)) + the int32 exponents (4(M + N)),
-        # over the stage's HIP-event duration (both slicing launches and the gap between them).
-        # traffic: the launches' measured HBM bytes (B's column maxima read B a second time at
-        # this shape), and the rate they move them at.
+        # over the stage's HIP-event duration (the slot-marking launch, the one-read slicing
+        # launch and the gap between them). traffic: the launches' measured HBM bytes (each
+        # input read once at this shape), and the rate they move them at.
         "slicing_roofline": {"bound": "hbm", "achieved": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9, 1),
                              "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": round(slice_bytes / (head["slice_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
