@@ -103,6 +103,10 @@ _SIGNATURES = {
                                      ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int,
                                      ctypes.c_void_p]),
     "rg_test_set_spin_limit": (ctypes.c_int, [ctypes.c_int]),
+    "rg_test_pslice_placement": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                ctypes.POINTER(rg_config), ctypes.c_int,
+                                                ctypes.c_int, ctypes.POINTER(ctypes.c_longlong),
+                                                ctypes.POINTER(ctypes.c_longlong)]),
     "rg_plan_for_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_config), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(rg_plan),

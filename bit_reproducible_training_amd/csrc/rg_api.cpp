@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "repro_gemm.h"
 #include "rg_internal.h"
@@ -645,6 +646,49 @@ int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950
         coords[4 * i + 1] = part;
         coords[4 * i + 2] = tm;
         coords[4 * i + 3] = tn;
+    }
+    return hipSuccess;
+}
+
+int rg_test_pslice_placement(int M, int N, int K, const rg_config* cfg, int num_cus, int batch,
+                             long long* blocks, long long* split_panels) {
+    if (!cfg || !blocks || !split_panels) return hipErrorInvalidValue;
+    rg::DeviceInfo dev{true, num_cus};
+    rg::PlanExtras extras;
+    extras.batch = batch;
+    rg::Layout L;
+    const int e = rg::plan_layout(M, N, K, cfg->split_k, cfg->tile_m, cfg->tile_n, cfg->algo,
+                                  cfg->slices, cfg->trans_a != 0, cfg->trans_b != 0, dev, &L,
+                                  extras);
+    if (e != hipSuccess) return e;
+    *blocks = 0;
+    *split_panels = 0;
+    const struct {
+        int parts, Rp;
+        bool strided;
+    } ops[2] = {{L.ps_a, L.Mp, L.a_strided}, {L.ps_b, L.Np, L.b_strided}};
+    for (const auto& op : ops) {
+        if (op.parts <= 0) continue;
+        rg::SliceDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.Rp = op.Rp;
+        d.Kp = L.Kp;
+        d.batch = L.batch;
+        d.strided = op.strided ? 1 : 0;
+        rg::pslice_grid(d);
+        const long long panels = (long long)d.batch * (d.Rp / (d.strided ? rg::PANEL_ROWS : 8));
+        std::vector<int> xcd((size_t)panels, -1);
+        for (long long blk = 0; blk < d.ps_blocks; ++blk) {
+            const long long u = rg::pslice_unit(blk, d.ps_blocks);
+            if (u >= panels * d.ps_parts) continue;
+            int& x = xcd[(size_t)(u / d.ps_parts)];
+            if (x == -1) x = (int)(blk & 7);
+            else if (x != (int)(blk & 7) && x != 8) {
+                x = 8;  // seen on two XCDs
+                ++*split_panels;
+            }
+        }
+        *blocks += d.ps_blocks;
     }
     return hipSuccess;
 }

@@ -270,6 +270,13 @@ int slice_spin_limit();
 void set_slice_spin_limit(int polls);
 // Fills ps_parts / ps_blocks of d (spin_limit is the caller's).
 void pslice_grid(SliceDesc& d);
+// Unit of one-read slicing block blk (units: panel or strip x part, in panel order). Block blk
+// runs on XCD blk % 8, and each XCD takes a contiguous range of ps_blocks / 8 units, which
+// pslice_grid makes a whole number of panels (or strips): the parts of a panel, which exchange
+// their maxima through the XCD's L2, then all run on one XCD.
+__host__ __device__ inline long long pslice_unit(long long blk, long long ps_blocks) {
+    return (blk & 7) * (ps_blocks / 8) + (blk >> 3);
+}
 // The partial-maximum slots the one read of d waits on.
 MarkRange pslice_slots(const SliceDesc& d);
 void launch_pslice(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_b, int S,

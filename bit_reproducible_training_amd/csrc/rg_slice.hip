@@ -863,9 +863,10 @@ void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hi
 // maximum is exact and order-free), so no block depends on another being resident or visible.
 // Part 0 writes the exponents.
 // Blocks run on XCD blk % 8 (the dispatcher deals workgroups to the XCDs in turn) and each XCD
-// takes a contiguous range of (panel, part) in panel order (ps_blocks is a multiple of 8), so a
-// panel's parts are dispatched one after another on one XCD, and the neighbouring panels of an
-// unaligned operand, which share the lines at their edges, run on one XCD too. The slots are
+// takes a contiguous range of (panel, part) in panel order, a whole number of panels
+// (pslice_unit), so a panel's parts are dispatched one after another on one XCD, and the
+// neighbouring panels of an unaligned operand, which share the lines at their edges, run on one
+// XCD too. The slots are
 // therefore written with plain stores, which land in the XCD's L2 (the compute unit's L1 is
 // write-through), and polled with non-temporal loads, which skip the L1 (where a polled line
 // would stay stale) and are served by that L2. A device-scope exchange instead goes to the
@@ -912,7 +913,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
     const int npk = d.Kp / PANEL_K;
     const int parts = d.ps_parts;
     const long long rpanels = (long long)d.batch * (d.Rp / PANEL_ROWS);
-    const long long lin = (blk & 7) * (d.ps_blocks / 8) + (blk >> 3);
+    const long long lin = pslice_unit(blk, d.ps_blocks);
     if (lin >= rpanels * parts) return;  // padding block (whole block)
     const int rp = (int)(lin / parts), part = (int)(lin - (long long)rp * parts);
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -1010,7 +1011,7 @@ __device__ void pslice_rows(const SliceDesc& d, long long blk) {
     const int parts = d.ps_parts;
     const int per_item = d.Rp / 8;
     const long long nstrips = (long long)d.batch * per_item;
-    const long long lin = (blk & 7) * (d.ps_blocks / 8) + (blk >> 3);
+    const long long lin = pslice_unit(blk, d.ps_blocks);
     if (lin >= nstrips * parts) return;  // padding block (whole block)
     const long long st = lin / parts;
     const int part = (int)(lin - st * parts);
@@ -1157,8 +1158,10 @@ void set_slice_spin_limit(int polls) { g_spin_limit = polls < 0 ? 0 : polls; }
 
 void pslice_grid(SliceDesc& d) {
     d.ps_parts = pslice_parts(d.strided != 0, d.Kp);
-    const long long units = (long long)d.batch * (d.Rp / (d.strided ? PANEL_ROWS : 8)) * d.ps_parts;
-    d.ps_blocks = (units + 7) / 8 * 8;
+    // Whole panels (strips) per XCD: a panel's parts must not be split between two XCDs, whose
+    // L2s do not see each other's slots (they would wait out their bound and re-read K).
+    const long long panels = (long long)d.batch * (d.Rp / (d.strided ? PANEL_ROWS : 8));
+    d.ps_blocks = 8 * ((panels + 7) / 8 * d.ps_parts);
 }
 
 MarkRange pslice_slots(const SliceDesc& d) {

@@ -128,6 +128,16 @@ int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950,
 int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950, int num_cus,
                         int batch, int* coords, long long capacity, long long* blocks);
 
+/* Test hook, no counterpart in the reference: where the one-read slicing (operands whose padded
+ * K is past the one-pass limit) places its blocks, for the plan rg_test_block_order makes (same
+ * arguments). *blocks receives the one-read blocks of both operands (0 when neither takes that
+ * route) and *split_panels the number of row panels (strips of 8 rows for row access) whose
+ * parts along K run on more than one XCD (workgroup i on XCD i mod 8); such parts cannot see
+ * each other's partial maxima and each waits out its bound. Host only; 1 (invalid value) as
+ * rg_test_block_order. */
+int rg_test_pslice_placement(int M, int N, int K, const rg_config* cfg, int num_cus, int batch,
+                             long long* blocks, long long* split_panels);
+
 /* Test hook, no counterpart in the reference: the GPU epilogue's final rounding on arrays,
  * so tests can compare it with round_to_float on chosen inputs. Exactly one of levels and T
  * is non-NULL. levels: n x (2S-1) int32 level sums per output, most significant first, rounded

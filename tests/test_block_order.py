@@ -114,3 +114,51 @@ def test_resident_blocks_share_panels(M, N, K, kw):
         assert np.array_equal(coords, plain)
     if N == 768 and K <= 3072:
         assert ours * 3 <= base * 2
+
+
+# Shapes whose long operands take the one-read slicing (padded K past the one-pass limit), with
+# panel counts that are and are not multiples of 8: the headline, the GPT-2 weight gradients,
+# the LM head's (1571 column panels of 8 parts), a ragged batch, and the convolution weight
+# gradients of the widened benchmark (LeNet conv2: 10000 windows, 150 and 16 columns; ResNet-like
+# 100352 windows is past the one-read limit and keeps two passes).
+PSLICE_SHAPES = [
+    (4096, 4096, 4096, 1, {}),
+    (768, 768, 8192, 1, {"trans_a": True}),
+    (2304, 768, 8192, 1, {"trans_a": True}),
+    (50257, 768, 8192, 1, {"trans_a": True}),
+    (1024, 1024, 65536, 1, {}),
+    (16, 150, 10000, 1, {"trans_a": True}),
+    (6, 150, 5000, 1, {"trans_a": True}),
+    (96, 40, 6000, 3, {"trans_b": True}),
+    (200, 70, 20000, 1, {}),
+]
+
+
+@pytest.mark.parametrize("M,N,K,batch,kw", PSLICE_SHAPES)
+@pytest.mark.parametrize("num_cus", [256, 304, 80])
+def test_one_read_slicing_keeps_each_panel_on_one_xcd(M, N, K, batch, kw, num_cus):
+    """The parts of a panel exchange their partial maxima through their XCD's L2, so the
+    one-read slicing must run all of them on one XCD (workgroup i on XCD i mod 8): with a panel
+    split between two XCDs each part waits out its bound and re-reads the panel's whole K (the
+    same bits, about 1 ms later; LeNet conv2's weight gradient took 3.2 ms instead of 0.04)."""
+    cfg = rg.Config(**kw).to_c()
+    blocks, split = ctypes.c_longlong(), ctypes.c_longlong()
+    code = lib.rg_test_pslice_placement(M, N, K, ctypes.byref(cfg), num_cus, batch,
+                                        ctypes.byref(blocks), ctypes.byref(split))
+    assert code == 0
+    assert blocks.value % 8 == 0
+    assert split.value == 0, (blocks.value, split.value)
+
+
+def test_one_read_slicing_placement_hook_sees_the_routes():
+    """The hook reports blocks exactly when an operand takes the one-read route: none at K = 1024
+    (one pass), some at 4096^3 NN (B, column access) and for a transposed A over K = 8192."""
+    def blocks(M, N, K, **kw):
+        cfg = rg.Config(**kw).to_c()
+        b, s = ctypes.c_longlong(), ctypes.c_longlong()
+        assert lib.rg_test_pslice_placement(M, N, K, ctypes.byref(cfg), 256, 1, ctypes.byref(b),
+                                            ctypes.byref(s)) == 0
+        return b.value
+    assert blocks(1024, 1024, 1024) == 0
+    assert blocks(4096, 4096, 4096) > 0
+    assert blocks(768, 768, 8192, trans_a=True) > 0
