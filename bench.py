@@ -46,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "70c5caaaecae614686e05fab758834f13b42f67f24904688ff51d5482bc88f82"),
-    "slicing": (235581338, ("rg_slice.hip", "rg_internal.h"),
-                "bbfed543b8d3b8c45ce1a3b7c0725e982ea4514b00011432919f77b153ba2564"),
+                 "7f544a1eb6094acf37de88a096e9ae12345923830c7852ac77dd7e8f009e6a6c"),
+    "slicing": (235582669, ("rg_slice.hip", "rg_internal.h"),
+                "13d2628152ce9ade8805a7b7b4d8f9590ccc6435c8f83c8b2d5f58eca28abd51"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
