@@ -176,7 +176,9 @@ int rg_gemm_strided_batched_fp32_ws(const float* A, long long lda, long long str
 /* No counterpart in the reference: rg_gemm_fp32_ws for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * The workspace is a fixed device array inside the library, RG_NOALLOC_SCRATCH_BYTES (128 MiB)
- * on each GPU, held from the first call on that GPU until the process ends; this entry point
+ * on each GPU, held from the first call on that GPU until the process ends (the array sits in
+ * a code object of its own, loaded on that first call: loading the library or running the
+ * other entry points reserves none of it); this entry point
  * calls no hipMalloc/hipFree and no allocating library routine. The caller passes A, B, C as
  * for rg_gemm_fp32_ws. Returns 1 (invalid value) when the plan's workspace_bytes
  * (rg_make_plan) exceeds RG_NOALLOC_SCRATCH_BYTES (4096^3 at S = 3 needs about 96 MiB), or

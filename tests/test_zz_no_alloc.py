@@ -75,6 +75,21 @@ def test_noalloc_first_call_under_graph_capture(torch_gpu):
     assert r.returncode == 0 and "noalloc capture ok" in r.stdout, r.stdout[-2000:]
 
 
+def test_noalloc_scratch_is_reserved_at_its_first_use(torch_gpu):
+    """The 128 MiB scratch array is reserved on a GPU when the entry point is first called
+    there, not when the library is loaded or a plain GEMM runs (fresh worker process; measured
+    with torch.cuda.mem_get_info)."""
+    import os
+    import subprocess
+    import sys
+
+    worker = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_reserve_worker.py")
+    note("noalloc scratch reservation (worker process)")
+    r = subprocess.run([sys.executable, worker], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True, timeout=300)
+    assert r.returncode == 0 and "noalloc reserve ok" in r.stdout, r.stdout[-2000:]
+
+
 def test_noalloc_refuses_plans_beyond_the_scratch(torch_gpu):
     torch = torch_gpu
     M = N = K = 8192                     # digit panels alone: 2 * 8192 * 8192 * 3 B = 384 MiB
