@@ -21,9 +21,11 @@ from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-# Padded K from just past the column one-pass limit (3072) to several parts of 1024 k.
+# Padded K from just past the column one-pass limit (3072) to several parts of 1024 k, and past
+# 32 parts (K > 32768), where a column-access operand keeps the two passes next to the other
+# operand's one read (row access) or two passes.
 SHAPES = [(64, 100, 3076), (33, 200, 4096), (100, 33, 5000), (130, 70, 8193), (32, 32, 3073),
-          (70, 45, 4097), (24, 40, 12289), (9, 17, 20000)]
+          (70, 45, 4097), (24, 40, 12289), (9, 17, 20000), (40, 33, 40000), (20, 64, 65536)]
 
 
 def _check_slices(torch, A, B, M, N, K, ta, tb, S, ws_fill=None):
@@ -71,7 +73,7 @@ def test_one_read_slicing_against_oracle(torch_gpu, M, N, K, ta, tb, S):
 
 @pytest.mark.parametrize("M,N,K,ta,tb", [(64, 100, 3076, 0, 0), (130, 70, 8193, 1, 0),
                                          (100, 33, 5000, 1, 1), (40, 70, 9000, 0, 1),
-                                         (33, 20, 17000, 0, 0)])
+                                         (33, 20, 17000, 0, 0), (20, 40, 50000, 1, 0)])
 def test_one_read_slicing_fallback(torch_gpu, M, N, K, ta, tb):
     """Wait bound 0: every block takes the fallback; same digits and bits."""
     A, B = _inputs(M, N, K, 99 + K)
@@ -89,7 +91,8 @@ def test_one_read_slicing_on_garbage_workspace(torch_gpu, fill):
     like a published maximum): the call marks them empty itself before the one read, whether the
     other operand takes the one pass in the same launch or the one read too."""
     torch = torch_gpu
-    for M, N, K, ta, tb in [(96, 64, 4100, 0, 0), (64, 96, 6000, 1, 0), (64, 96, 6000, 0, 1)]:
+    for M, N, K, ta, tb in [(96, 64, 4100, 0, 0), (64, 96, 6000, 1, 0), (64, 96, 6000, 0, 1),
+                            (32, 40, 40000, 0, 0)]:
         A, B = _inputs(M, N, K, fill + K)
         for rep in range(2):
             note("pslice garbage fill=%d M=%d N=%d K=%d ta=%d tb=%d rep %d" % (fill, M, N, K, ta, tb, rep))
