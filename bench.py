@@ -46,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "7f544a1eb6094acf37de88a096e9ae12345923830c7852ac77dd7e8f009e6a6c"),
-    "slicing": (235582669, ("rg_slice.hip", "rg_internal.h"),
-                "13d2628152ce9ade8805a7b7b4d8f9590ccc6435c8f83c8b2d5f58eca28abd51"),
+                 "342f87ff93dc965495099c75df9a4eb56bd21b0150bab4fab49891b258d9a2bc"),
+    "slicing": (235611136, ("rg_slice.hip", "rg_internal.h"),
+                "44e2fd4717aec75c6aee50edd97fca650ea62a5b5e9831e01ac92127a7f0140e"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 

@@ -263,8 +263,10 @@ __host__ __device__ inline bool pslice_route(bool strided, int Kp) {
 }
 // Polls of a block's wait for the other parts of its panel before it reads their k ranges
 // itself (rg_test_set_spin_limit sets it; 0: no exchange, every block reads its panel's whole K
-// for the maxima). A poll takes about 0.45 us on MI355X, so the default bounds the wait near
-// 1 ms, far past a normal wait (parts that load together publish within a few tens of us).
+// for the maxima). A poll (one L2 round trip per eight parts, then a short sleep) took about
+// 0.45 us on MI355X when it read the slots one at a time, so the default bounds the wait at
+// about 1 ms or less, far past a normal wait (parts that load together publish within a few
+// tens of us).
 constexpr int DEFAULT_SPIN_LIMIT = 2048;
 int slice_spin_limit();
 void set_slice_spin_limit(int polls);
