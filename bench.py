@@ -46,7 +46,7 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "342f87ff93dc965495099c75df9a4eb56bd21b0150bab4fab49891b258d9a2bc"),
+                 "725de9246aac9d91597cbc72be3d2e42b2fafe1e43818798bcb5a4171a751361"),
     "slicing": (235611136, ("rg_slice.hip", "rg_internal.h"),
                 "44e2fd4717aec75c6aee50edd97fca650ea62a5b5e9831e01ac92127a7f0140e"),
 }

@@ -391,13 +391,17 @@ contract_mfma(const int8_t* __restrict__ QA, const int8_t* __restrict__ QB,
                             v[i] = round_to_float_rare(combine_levels<L>(lv), er[4 * q + i] + ec[tj]);
                         }
                     }
+                    // Non-temporal stores: C is not read again here, and streaming it past the
+                    // caches made the contraction faster (4096^3 steady state 0.466 -> 0.459 ms,
+                    // 8192x3072x768 NT 0.166 -> 0.158 ms, LM-head forward -1.5%; A/B on one box).
                     if (inside) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) cp[(size_t)(8 * q + i) * ldc] = v[i];
+                        for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(v[i], &cp[(size_t)(8 * q + i) * ldc]);
                     } else if (col[tj] < N) {
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
-                            if (rows_inside || row0 + ti * 32 + 8 * q + i < M) cp[(size_t)(8 * q + i) * ldc] = v[i];
+                            if (rows_inside || row0 + ti * 32 + 8 * q + i < M)
+                                __builtin_nontemporal_store(v[i], &cp[(size_t)(8 * q + i) * ldc]);
                     }
                     // Keep the scheduler from hoisting every accumulator read to the top.
                     __builtin_amdgcn_sched_barrier(0);
