@@ -46,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "725de9246aac9d91597cbc72be3d2e42b2fafe1e43818798bcb5a4171a751361"),
-    "slicing": (235611136, ("rg_slice.hip", "rg_internal.h"),
-                "44e2fd4717aec75c6aee50edd97fca650ea62a5b5e9831e01ac92127a7f0140e"),
+                 "4af1c679f63f84df18057732a53256b4e748de5e57343c9932745da68f6948dc"),
+    "slicing": (235604173, ("rg_slice.hip", "rg_internal.h"),
+                "4374f5da23d69364806d995d51c215adae217e9fcc006cf629c6836411ce2a09"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 

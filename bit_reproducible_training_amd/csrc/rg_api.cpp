@@ -485,8 +485,8 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
         if (opt.group_b > 0) launch_group_max(db, opt.group_b, stream);
         launch_split(none, db, L.S, i32, stream);
     } else if (ps_a || ps_b) {
-        // one operand in one read, the other in two passes (column access past the one read's
-        // part limit, or group scales): the one read and the other's maxima in one launch,
+        // one operand in one read, the other in two passes (past the one read's part limit,
+        // or group scales): the one read and the other's maxima in one launch,
         // then the other's split (1024x1024x65536 NN slicing 287 -> ~230 us)
         const SliceDesc& ps = ps_a ? da : db;
         const SliceDesc& two = ps_a ? db : da;
@@ -676,6 +676,10 @@ int rg_test_pslice_placement(int M, int N, int K, const rg_config* cfg, int num_
         d.batch = L.batch;
         d.strided = op.strided ? 1 : 0;
         rg::pslice_grid(d);
+        if (d.ps_dev) {  // spread over every XCD by design, exchanging through memory
+            *blocks += d.ps_blocks;
+            continue;
+        }
         const long long panels = (long long)d.batch * (d.Rp / (d.strided ? rg::PANEL_ROWS : 8));
         std::vector<int> xcd((size_t)panels, -1);
         for (long long blk = 0; blk < d.ps_blocks; ++blk) {

@@ -874,7 +874,11 @@ void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hi
 // XCD's whole L2 while the launch's other blocks fill it with digits. A block whose parts ran on
 // another XCD can only see PM_EMPTY or this call's maxima (the slots were marked by an earlier
 // launch, whose writes the launch boundary made visible everywhere), so at worst it takes the
-// fallback: placement never changes a bit.
+// fallback: placement never changes a bit. A column-access operand with more parts than one
+// XCD holds at once (ps_dev) runs its panels' parts in the plain order instead, i.e. spread over
+// every XCD, and exchanges at device scope: the slot store is written through to memory and the
+// polls miss the L2 (scope bit sc1 on those instructions only; no cache-wide write-back or
+// invalidate).
 // Eight slot words read past the L1 with one wait: a poll costs one round trip per eight parts
 // (the LM head's weight gradient, 8 parts: slicing 0.605 -> 0.595 ms against four per wait,
 // 0.65 ms with one).
@@ -894,10 +898,35 @@ __device__ __forceinline__ void load8_bypass_l1(const unsigned* const (&p)[8], u
         : "memory");
 }
 
+// Device scope (sc1): a store written through to memory and loads that miss the XCD's L2, for
+// parts that run on different XCDs; no cache-wide write-back or invalidate.
+__device__ __forceinline__ void load8_device(const unsigned* const (&p)[8], unsigned (&v)[8]) {
+    asm volatile(
+        "global_load_dword %0, %8, off sc1\n\t"
+        "global_load_dword %1, %9, off sc1\n\t"
+        "global_load_dword %2, %10, off sc1\n\t"
+        "global_load_dword %3, %11, off sc1\n\t"
+        "global_load_dword %4, %12, off sc1\n\t"
+        "global_load_dword %5, %13, off sc1\n\t"
+        "global_load_dword %6, %14, off sc1\n\t"
+        "global_load_dword %7, %15, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7])
+        : "memory");
+}
+__device__ __forceinline__ void store_device(unsigned* p, unsigned v) {
+    asm volatile("global_store_dword %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride, int part, int parts,
-                                               int spin_limit, int lane, int nl, float* mm) {
+                                               int spin_limit, int lane, int nl, float* mm,
+                                               bool dev = false) {
     if (spin_limit <= 0) return false;
-    if (lane < nl) pm[(size_t)part * part_stride] = __float_as_uint(*mm);
+    if (lane < nl) {
+        if (dev) store_device(pm + (size_t)part * part_stride, __float_as_uint(*mm));
+        else pm[(size_t)part * part_stride] = __float_as_uint(*mm);
+    }
     for (int n = 0;; ++n) {
         float m = *mm;
         bool seen = true;
@@ -908,7 +937,8 @@ __device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride,
 #pragma unroll
                 for (int j = 0; j < 8; ++j) q[j] = pm + (size_t)min(p0 + j, parts - 1) * part_stride;
                 unsigned v[8];
-                load8_bypass_l1(q, v);
+                if (dev) load8_device(q, v);
+                else load8_bypass_l1(q, v);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     if (p0 + j >= parts || p0 + j == part) continue;
@@ -934,7 +964,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
     const int npk = d.Kp / PANEL_K;
     const int parts = d.ps_parts;
     const long long rpanels = (long long)d.batch * (d.Rp / PANEL_ROWS);
-    const long long lin = pslice_unit(blk, d.ps_blocks);
+    const long long lin = pslice_unit(blk, d.ps_blocks, d.ps_dev != 0);
     if (lin >= rpanels * parts) return;  // padding block (whole block)
     const int rp = (int)(lin / parts), part = (int)(lin - (long long)rp * parts);
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -981,7 +1011,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
         int ok = 1;
         if (parts > 1) {
             unsigned* pm = reinterpret_cast<unsigned*>(d.pmax) + rp * PANEL_ROWS + (lane & 31);
-            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, 32, &mm) ? 1 : 0;
+            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, 32, &mm, d.ps_dev != 0) ? 1 : 0;
         }
         if (lane < 32) sfin[lane] = mm;
         if (lane == 0) sok = ok;
@@ -1179,6 +1209,11 @@ void set_slice_spin_limit(int polls) { g_spin_limit = polls < 0 ? 0 : polls; }
 
 void pslice_grid(SliceDesc& d) {
     d.ps_parts = pslice_parts(d.strided != 0, d.Kp);
+    d.ps_dev = d.strided && d.ps_parts > PS_MAX_PARTS ? 1 : 0;
+    if (d.ps_dev) {  // plain order: consecutive parts of a panel on consecutive XCDs
+        d.ps_blocks = ((long long)d.batch * (d.Rp / PANEL_ROWS) * d.ps_parts + 7) / 8 * 8;
+        return;
+    }
     // Whole panels (strips) per XCD: a panel's parts must not be split between two XCDs, whose
     // L2s do not see each other's slots (they would wait out their bound and re-read K).
     const long long panels = (long long)d.batch * (d.Rp / (d.strided ? PANEL_ROWS : 8));

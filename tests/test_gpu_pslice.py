@@ -3,7 +3,8 @@
 An operand whose padded K is past the one-pass limit (column access: op(B) of an NN or TN GEMM,
 op(A) of a TN or TT GEMM, past 3072; row access past 4096) is read once: blocks hold a 32-column
 panel or an 8-row strip over a range of k in registers, and the blocks of a panel exchange their
-partial maxima through slots in the workspace that the call marks empty first. Checked against
+partial maxima through slots in the workspace that the call marks empty first (through the
+XCD's L2, or through memory for column-access operands of more than 32 parts). Checked against
 the oracle: every digit of both operands' panels, the exponents, the zero padding and the
 GEMM's bits, at S = 1..3, over every transpose, for K just past the limits, K with a partial
 last part, ragged panels and long K; the same with the wait bound set to zero (every block then
@@ -22,8 +23,8 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 # Padded K from just past the column one-pass limit (3072) to several parts of 1024 k, and past
-# 32 parts (K > 32768), where a column-access operand keeps the two passes next to the other
-# operand's one read (row access) or two passes.
+# 32 parts (K > 32768), where a column-access operand's parts run on every XCD and exchange
+# their maxima at device scope.
 SHAPES = [(64, 100, 3076), (33, 200, 4096), (100, 33, 5000), (130, 70, 8193), (32, 32, 3073),
           (70, 45, 4097), (24, 40, 12289), (9, 17, 20000), (40, 33, 40000), (20, 64, 65536)]
 
