@@ -35,6 +35,55 @@ __device__ __forceinline__ unsigned max4_bits(float4 v) {
     return max(max(a, b), max(c, e));
 }
 
+// The four values q[k .. k+3] of a row of K values, zero past either end of the row. q + k is
+// 16-byte aligned (callers choose k so); the vector load is taken only where all four values lie
+// inside the row, otherwise the values inside are read one by one.
+__device__ __forceinline__ float4 load4_in_row(const float* q, int k, int K) {
+    if (k >= 0 && k + 3 < K) return *reinterpret_cast<const float4*>(q + k);
+    float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (k >= 0 && k < K) t.x = q[k];
+    if (k + 1 >= 0 && k + 1 < K) t.y = q[k + 1];
+    if (k + 2 >= 0 && k + 2 < K) t.z = q[k + 2];
+    if (k + 3 >= 0 && k + 3 < K) t.w = q[k + 3];
+    return t;
+}
+
+// Row access where rows are not 16-byte aligned (K or ld not a multiple of 4, or an unaligned
+// base): v[i] = q[kb + 32i + 4g .. +3] (g = lane % 8, the lane's place among the eight lanes of
+// its row; kb a multiple of 32), zero at k >= K, read by whole aligned 16-byte loads instead of
+// four scalar loads per lane. Each lane loads the aligned vector that holds its first value
+// (starting o values earlier, o = the row's misalignment in floats) and takes the values it
+// lacks from the aligned vector of the next lane of its row, which for g = 7 is lane g = 0's
+// vector of the next k panel (lane g = 0 loads one vector past the last panel for it). Every
+// lane of the wavefront must call this (the exchange is a cross-lane read); a lane whose row
+// is dead (live false) reads nothing and gets zeros. Used by the one read of row-access operands
+// (8192x768x50257 NN, A's 8192 rows of 50257 values: slicing 889 -> 759 us against four scalar
+// loads per lane).
+template <int NF>
+__device__ __forceinline__ void load_row_realigned(const float* q, int K, int kb, int lane, bool live,
+                                                   float4 (&v)[NF]) {
+    const int g = lane & 7;
+    const int o = live ? (int)((reinterpret_cast<uintptr_t>(q) >> 2) & 3) : 0;
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < NF; ++i) v[i] = live ? load4_in_row(q, kb + 32 * i + 4 * g - o, K) : zero;
+    const float4 tail = live && g == 0 ? load4_in_row(q, kb + 32 * NF - o, K) : zero;
+    const int src = (lane & ~7) | ((g + 1) & 7);
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+        // what this lane hands to the lane before it (g = 0: to g = 7, from the next panel);
+        // v[i + 1] is still the aligned vector here, v[i] is replaced below
+        const float4 give = g == 0 ? (i + 1 < NF ? v[i + 1] : tail) : v[i];
+        const float n0 = __shfl(give.x, src, 64), n1 = __shfl(give.y, src, 64);
+        const float n2 = __shfl(give.z, src, 64);
+        const float4 a = v[i];
+        v[i] = o == 0 ? a
+             : o == 1 ? make_float4(a.y, a.z, a.w, n0)
+             : o == 2 ? make_float4(a.z, a.w, n0, n1)
+                      : make_float4(a.w, n0, n1, n2);
+    }
+}
+
 // Exponent of stacked row q from its maximum m (which skips NaN), or 0 where d.nanrows flags
 // the row.
 __device__ __forceinline__ int row_exponent(const SliceDesc& d, size_t q, float m) {
@@ -600,7 +649,9 @@ __device__ void slice_onepass(const SliceDesc& d, long long blk) {
                     } else {
                         v[i] = *reinterpret_cast<const float4*>(q);
                     }
-                } else {  // unaligned rows or K % 4 != 0: four scalar loads inside K
+                } else {  // unaligned rows or K % 4 != 0: four scalar loads inside K (in the one
+                          // pass they cost no more than load_row_realigned: 8192 rows, K = 4095,
+                          // 1-2 us faster; K = 767 within 1 us)
                     v[i].x = q[0];
                     if (k + 1 < d.K) v[i].y = q[1];
                     if (k + 2 < d.K) v[i].z = q[2];
@@ -1077,21 +1128,15 @@ __device__ void pslice_rows(const SliceDesc& d, long long blk) {
     const int row = r0 + (lane >> 3);
     float4 v[PS_ROW_NF4];
     float m = 0.0f;
+    if (d.vec) {
 #pragma unroll
-    for (int i = 0; i < PS_ROW_NF4; ++i) {
-        const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
-        v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (row < d.R && k < d.K) {
-            const float* q = base + (size_t)row * d.ld + k;
-            if (d.vec) {
-                v[i] = *reinterpret_cast<const float4*>(q);
-            } else {  // unaligned rows or K % 4 != 0: four scalar loads inside K
-                v[i].x = q[0];
-                if (k + 1 < d.K) v[i].y = q[1];
-                if (k + 2 < d.K) v[i].z = q[2];
-                if (k + 3 < d.K) v[i].w = q[3];
-            }
+        for (int i = 0; i < PS_ROW_NF4; ++i) {
+            const int k = (kp0 + i) * PANEL_K + 4 * (lane & 7);
+            v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (row < d.R && k < d.K) v[i] = *reinterpret_cast<const float4*>(base + (size_t)row * d.ld + k);
         }
+    } else {  // rows not 16-byte aligned
+        load_row_realigned<PS_ROW_NF4>(base + (size_t)row * d.ld, d.K, kp0 * PANEL_K, lane, row < d.R, v);
     }
 #pragma unroll
     for (int i = 0; i < PS_ROW_NF4; ++i) m = fmaxf(m, max4(v[i]));
