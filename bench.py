@@ -47,8 +47,8 @@ CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
                  "4af1c679f63f84df18057732a53256b4e748de5e57343c9932745da68f6948dc"),
-    "slicing": (235604173, ("rg_slice.hip", "rg_internal.h"),
-                "4374f5da23d69364806d995d51c215adae217e9fcc006cf629c6836411ce2a09"),
+    "slicing": (235629670, ("rg_slice.hip", "rg_internal.h"),
+                "ca0dbb60a2f59a15fd74a65f985830cf9abeb3276d504bfd5bd28ff4caa93c77"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 
