@@ -171,6 +171,38 @@ bool small_path(int M, int N, int K, int batch, int split_k, int tile_m, int til
     return tiles <= std::max(1, num_cus);
 }
 
+// The band kernel (contract_band) can run the GEMM: op(A) read along rows, K within the band's
+// LDS panels, one item, the default split, a plain GEMM, and op(B)'s digit region addressable
+// with 32-bit offsets (Np columns of W-column blocks).
+bool band_eligible(int N, int K, int S, bool ta, int batch, int split_k, int algo, int W,
+                   const PlanExtras& extras) {
+    if (ta || batch != 1 || split_k != 1 || K > BAND_MAX_K || algo == RG_ALGO_TILED) return false;
+    if (!extras.one_launch || extras.raw || !extras.gemm_bound) return false;
+    if (W < 64 || W % 32 != 0) return false;
+    const long long np = (long long)ceil_div(N, W) * W;
+    return np * round_up(K, STEP_K) * S < (1ll << 31);
+}
+
+// Estimated time (microseconds) of the band kernel with G column groups of W columns, and of
+// the op(A) slicing that it saves against the tile plans (both read and write op(A) at about
+// 4.5 TB/s), to weigh it against plan_cost's best tile plan; any choice gives the same bits.
+// Blocks (one per compute unit) run in rounds; a round loads its bands of op(A) (32 rows of K
+// values each, HBM-bound), then each wavefront contracts its ceil(W / 256) column tiles, one step
+// per 32 values of k. Fitted on MI355X at S = 3 (the GPT-2 layers at 8192 tokens, K = 768:
+// 0.53 us per step, the band load about 5.6 us): it picks the band for N = 768 and 2304 (3-18%
+// faster than the 64x64 tiles plus op(A)'s slicing) and the 128x128 tiles for N = 3072 (2%
+// faster than the band).
+double band_cost(int M, int K, int S, int W, int G, int num_cus) {
+    const double blocks = (double)ceil_div(M, 32) * G;
+    const double slots = std::max(1, num_cus);
+    const double rounds = std::ceil(blocks / slots);
+    const double load_us = std::min(blocks, slots) * 32.0 * K * 4.0 / 4.5e6;
+    const double step_us = 0.05 + 0.48 * (S * S / 9.0);
+    const double steps = (double)ceil_div(W / 32, 8) * ceil_div(K, 32);
+    return rounds * (load_us + steps * step_us);
+}
+double slice_a_cost(int M, int K, int S) { return (double)M * K * (4 + S) / 4.5e6; }
+
 }  // namespace
 
 int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int algo, int S,
@@ -206,7 +238,13 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
     } else {
         if (!dev.gfx950) return hipErrorNotSupported;
         L.algo = algo == RG_ALGO_TILED ? RG_ALGO_TILED : RG_ALGO_TENSOR_CORE;
-        if (small_path(M, N, K, batch, split_k, tile_m, tile_n, algo, extras, dev.num_cus)) {
+        // A pinned 32 x W tile (W >= 64) asks for the band kernel with blocks of W columns.
+        if (tile_m == 32 && band_eligible(N, K, S, ta, batch, split_k, algo, tile_n, extras)) {
+            L.band_w = tile_n;
+            L.band_groups = ceil_div(N, tile_n);
+        }
+        if (L.band_w == 0 &&
+            small_path(M, N, K, batch, split_k, tile_m, tile_n, algo, extras, dev.num_cus)) {
             L.small = true;
             L.Mp = round_up(M, PANEL_ROWS);
             L.Np = round_up(N, PANEL_ROWS);
@@ -218,6 +256,13 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
             *Lp = L;
             return hipSuccess;
         }
+    }
+    if (L.band_w > 0) {
+        L.Mp = round_up(M, PANEL_ROWS);
+        L.Np = L.band_groups * L.band_w;
+        L.split = 1;
+        L.has_partial = false;
+    } else if (L.algo != RG_ALGO_REFERENCE) {
         const int nsteps = L.Kp / STEP_K;
         const int min_split = ceil_div(nsteps, max_steps_per_part(S));
         // Candidate block tiles: the forced one, or 128x128 and 64x64; candidate splits: the
@@ -294,6 +339,33 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
             L.xcd_chunk = std::max(1, dev.num_cus / 8) * blocks_per_cu(ti, tj, S);
             L.group_m = group_rows(L.xcd_chunk, ti, tj, tiles_m, tiles_n);
         }
+        // The band kernel instead, when the caller pinned no tile and it is estimated faster
+        // than this plan plus op(A)'s slicing (column groups: 1, 2, 4 or 8, W a multiple of 32).
+        const bool pinned = algo == RG_ALGO_TILED || pinned_tile(tile_m, tile_n, S) ||
+                            tile_m == 32;
+        if (!pinned && split_k == 1) {
+            double band_best = best + slice_a_cost(M, K, S);
+            for (int G = 1; G <= 8; G *= 2) {
+                const int W = round_up(ceil_div(N, G), 32);
+                if (G > 1 && W == round_up(ceil_div(N, G / 2), 32)) break;  // no narrower
+                if (!band_eligible(N, K, S, ta, batch, split_k, algo, W, extras)) continue;
+                const double t = band_cost(M, K, S, W, ceil_div(N, W), dev.num_cus);
+                if (t < band_best) {
+                    band_best = t;
+                    L.band_w = W;
+                    L.band_groups = ceil_div(N, W);
+                }
+            }
+            if (L.band_w > 0) {
+                L.ti = L.tj = 0;
+                L.Mp = round_up(M, PANEL_ROWS);
+                L.Np = L.band_groups * L.band_w;
+                L.split = 1;
+                L.has_partial = false;
+                L.xcd_chunk = 0;
+                L.group_m = 1;
+            }
+        }
     }
 
     const int rows_a = (int)std::min<long long>((long long)M * batch, 1 << 30);
@@ -309,7 +381,8 @@ int plan_layout(int M, int N, int K, int split_k, int tile_m, int tile_n, int al
     }
 
     const size_t q_elem = L.algo == RG_ALGO_REFERENCE ? sizeof(int32_t) : (size_t)S;
-    const size_t Mt = (size_t)L.Mp * batch, Nt = (size_t)L.Np * batch;  // stacked rows
+    // (the band kernel keeps op(A)'s digits and exponents in LDS: no op(A) regions)
+    const size_t Mt = L.band_w > 0 ? 0 : (size_t)L.Mp * batch, Nt = (size_t)L.Np * batch;
     size_t off = 0;
     L.qa = off;
     off += align_up(Mt * L.Kp * q_elem);
@@ -455,6 +528,20 @@ int gemm_launch(const float* A, const float* B, float* C, const Layout& L, char*
     db.nanrows = opt.nanrows_b;
     const OutAddr out{addr.ldc, addr.stride_c};
 
+    if (L.band_w > 0) {  // op(B)'s one pass, then op(A)'s slicing, contraction, rounding
+        if (opt.group_a > 0 || opt.group_b > 0 || opt.raw || opt.im2col_a || opt.nanrows_a ||
+            opt.nanrows_b || L.batch != 1 || L.K > BAND_MAX_K || !onepass_eligible(db))
+            return hipErrorInvalidValue;
+        record(0);
+        launch_onepass(db, false, db, true, L.S, stream);
+        record(1);
+        launch_contract_band(L, A, addr.lda, static_cast<const int8_t*>(qb), eb, C, addr.ldc,
+                             stream);
+        record(2);
+        record(3);
+        return hipGetLastError();
+    }
+
     record(0);
     // Operands sliced in one pass (short K), or in one read with parts along K (long K, column
     // access); the others (and group scales, and the reference algorithm's int32 values) take
@@ -590,8 +677,8 @@ int rg_make_plan(int M, int N, int K, const rg_config* cfg, rg_plan* plan) {
     plan->algo = L.algo;
     plan->split_k = L.split;
     plan->workspace_bytes = L.total;
-    plan->tile_m = L.small ? 32 : 64 * L.ti;
-    plan->tile_n = L.small ? 32 : 64 * L.tj;
+    plan->tile_m = L.small || L.band_w > 0 ? 32 : 64 * L.ti;
+    plan->tile_n = L.small ? 32 : (L.band_w > 0 ? L.band_w : 64 * L.tj);
     return hipSuccess;
 }
 
@@ -606,8 +693,8 @@ int rg_plan_for_device(int M, int N, int K, const rg_config* cfg, int is_gfx950,
     plan->algo = L.algo;
     plan->split_k = L.split;
     plan->workspace_bytes = L.total;
-    plan->tile_m = L.small ? 32 : 64 * L.ti;
-    plan->tile_n = L.small ? 32 : 64 * L.tj;
+    plan->tile_m = L.small || L.band_w > 0 ? 32 : 64 * L.ti;
+    plan->tile_n = L.small ? 32 : (L.band_w > 0 ? L.band_w : 64 * L.tj);
     if (info) {
         info->qa = L.qa;
         info->qb = L.qb;
@@ -633,7 +720,7 @@ int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950
                             cfg->slices, cfg->trans_a != 0, cfg->trans_b != 0, dev, &L, extras);
     if (e != hipSuccess) return e;
     *blocks = 0;
-    if (L.algo == RG_ALGO_REFERENCE || L.small) return hipSuccess;
+    if (L.algo == RG_ALGO_REFERENCE || L.small || L.band_w > 0) return hipSuccess;
     const int tiles_m = L.Mp / (64 * L.ti), tiles_n = L.Np / (64 * L.tj);
     const long long total = (long long)tiles_m * tiles_n * L.split * L.batch;
     *blocks = total;
@@ -768,8 +855,8 @@ int rg_make_plan_strided_batched(int M, int N, int K, int batch, const rg_config
     plan->algo = L.algo;
     plan->split_k = L.split;
     plan->workspace_bytes = L.total;
-    plan->tile_m = L.small ? 32 : 64 * L.ti;
-    plan->tile_n = L.small ? 32 : 64 * L.tj;
+    plan->tile_m = L.small || L.band_w > 0 ? 32 : 64 * L.ti;
+    plan->tile_n = L.small ? 32 : (L.band_w > 0 ? L.band_w : 64 * L.tj);
     return hipSuccess;
 }
 

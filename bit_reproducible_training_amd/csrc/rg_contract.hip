@@ -613,6 +613,211 @@ contract_small(SmallOperand a, SmallOperand b, float* __restrict__ C, int K, lon
 #endif
 }
 
+// Band kernel, for op(A) read along rows with K <= BAND_MAX_K and many rows (the GPT-2 layers'
+// forward and input-gradient GEMMs at K = 768). Block (band, g) owns the 32 rows
+// [32 band, 32 band + 32) of op(A) and the output columns [g W, (g + 1) W). It slices its rows
+// itself, as the one-pass slicing does (every value loaded once into registers, the rows'
+// maxima in LDS, scale_exponent, rounding, bit-field digits), into digit panels in LDS, where
+// they stay for the rest of the launch. op(B)'s digit panels (sliced by the launch before) are
+// streamed from the caches straight into registers, D steps ahead: wavefront w takes the block's
+// column tiles w, w + 8, ..., contracts each 32x32 tile over all of K with
+// V_MFMA_I32_32X32X32_I8 (the digit pairs of one level in one int32 accumulator, as in
+// contract_mfma) and rounds and stores it as soon as its last k panel is done. Against slicing
+// op(A) in a launch of its own and contracting 64x64 tiles in three rounds of blocks, the digits
+// of op(A) never go through memory and the GEMM is one round of blocks (one per compute unit).
+// The values, the integer sums and the rounding are the pipeline's, so are the bits.
+// The loads of op(B) go through a buffer resource over its digit region, so an offset out of
+// the region would read zeros instead of faulting.
+template <int S, int NSL>
+__global__ void __launch_bounds__(BAND_THREADS, 2)
+contract_band(const float* __restrict__ A, long long lda, int vec_a, const int8_t* __restrict__ QB,
+              int qb_bytes, const int* __restrict__ eB, float* __restrict__ C, long long ldc,
+              int M, int N, int K, int Kp_ws, int W, int groups) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int L = 2 * S - 1;
+    constexpr int D = BAND_DEPTH;
+    __shared__ v4i band[(BAND_MAX_K / PANEL_K) * S][64];  // [k panel * S + digit][lane]
+    __shared__ int rmax[32];  // bit patterns of the rows' maxima (non-negative floats)
+    __shared__ int sexp[32];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    // Workgroup i runs on XCD i mod 8: with groups dividing 8, an XCD streams one column group.
+    const int g = blockIdx.x % groups, bnd = blockIdx.x / groups;
+    const int r0 = bnd * 32;
+    const int nkp = (K + PANEL_K - 1) / PANEL_K;  // k panels holding some k < K
+    const int npk_ws = Kp_ws / PANEL_K;           // k panels per 32-column panel of QB
+    const int ntile = W / 32;
+    const int tc0 = g * ntile;                    // first column tile of the block
+    const int my_tiles = ntile > wave ? (ntile - wave + 7) / 8 : 0;
+    const int total = my_tiles * nkp;             // (tile, k panel) steps of this wavefront
+    auto tile_of = [&](int j) RG_INLINE { return tc0 + wave + 8 * j; };
+
+    // op(B)'s panels of this wavefront's steps, fetched D steps ahead, in step order.
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)QB, (short)0, qb_bytes, 0x00020000);
+    const uint32_t voff = (uint32_t)lane * 16u;
+    int pj = 0, pk = 0;  // next (tile of this wavefront, k panel) to fetch
+    auto fetch = [&](v4i (&buf)[S]) RG_INLINE {
+        const uint32_t base =
+            (uint32_t)((tile_of(pj) * npk_ws + pk) * S) * (uint32_t)PANEL_BYTES;
+#pragma unroll
+        for (int q = 0; q < S; ++q)
+            buf[q] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, base + q * PANEL_BYTES, 0);
+        if (++pk == nkp) {
+            pk = 0;
+            ++pj;
+        }
+    };
+    v4i bq[D][S];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (d < total) fetch(bq[d]);
+    int ec = 0;  // column exponent (lane % 32) of the current tile
+    if (total > 0) ec = eB[tile_of(0) * 32 + (lane & 31)];
+
+    // Slicing of the band: slot i = t + BAND_THREADS j is lane s = i % 64 of k panel i / 64,
+    // i.e. row s % 32 and k = 32 (i / 64) + 16 (s / 32) .. + 15. Every load is issued first.
+    if (t < 32) rmax[t] = 0;
+    __syncthreads();
+    float x[NSL][16];
+#pragma unroll
+    for (int j = 0; j < NSL; ++j) {
+        const int i = t + BAND_THREADS * j;
+        const int kp = i >> 6, s = i & 63;
+        const int r = r0 + (s & 31), k0 = kp * PANEL_K + 16 * (s >> 5);
+        const bool live = kp < nkp && r < M;
+        const float* row = A + (size_t)r * lda;
+        if (live && vec_a) {
+            const float4* p = reinterpret_cast<const float4*>(row + k0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (k0 + 4 * q < K) v = p[q];  // K % 4 == 0: a float4 is wholly in or out
+                x[j][4 * q] = v.x;
+                x[j][4 * q + 1] = v.y;
+                x[j][4 * q + 2] = v.z;
+                x[j][4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) x[j][e] = (live && k0 + e < K) ? row[k0 + e] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NSL; ++j) {
+        const int i = t + BAND_THREADS * j;
+        if ((i >> 6) < nkp) {
+            float m = 0.0f;  // the maximum skips NaN (fmaxf), as the definition's CPU path does
+#pragma unroll
+            for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(x[j][e]));
+            atomicMax(&rmax[i & 31], __float_as_int(m));
+        }
+    }
+    __syncthreads();
+    if (t < 32) sexp[t] = repro_gemm::scale_exponent(__int_as_float(rmax[t]));  // rows past M: 0
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NSL; ++j) {
+        const int i = t + BAND_THREADS * j;
+        const int kp = i >> 6, s = i & 63;
+        if (kp < nkp) {
+            const RowScale rs = row_scale<S>(sexp[s & 31]);
+            int dg[S][16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                int dd[S];
+                digits_of<S>(round_fixed(x[j][e], rs), dd);
+#pragma unroll
+                for (int p = 0; p < S; ++p) dg[p][e] = dd[p];
+            }
+#pragma unroll
+            for (int p = 0; p < S; ++p) {
+                v4i w;
+                w[0] = (int)pack4(dg[p][0], dg[p][1], dg[p][2], dg[p][3]);
+                w[1] = (int)pack4(dg[p][4], dg[p][5], dg[p][6], dg[p][7]);
+                w[2] = (int)pack4(dg[p][8], dg[p][9], dg[p][10], dg[p][11]);
+                w[3] = (int)pack4(dg[p][12], dg[p][13], dg[p][14], dg[p][15]);
+                band[kp * S + p][s] = w;
+            }
+        }
+    }
+    __syncthreads();
+
+    // Exponents of this lane's output rows: register e of a 32x32 accumulator tile holds row
+    // 8 (e / 4) + 4 (lane / 32) + e % 4, column lane % 32.
+    const int e0 = -14 * (S - 1);
+    int er[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) er[e] = sexp[8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)] + e0;
+
+    v16i acc[L];
+    int jt = 0, ks = 0;  // current tile of this wavefront, k panel
+    auto epilogue = [&]() RG_INLINE {
+        const int col = tile_of(jt) * 32 + (lane & 31);
+        const int rbase = r0 + 4 * (lane >> 5);
+        float* cp = C + (size_t)rbase * ldc + col;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float v[4];
+            bool all_ok = true;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int lv[L];
+#pragma unroll
+                for (int l = 0; l < L; ++l) lv[l] = acc[l][4 * q + i];
+                bool ok;
+                v[i] = round_levels_try<L>(lv, er[4 * q + i] + ec, &ok);
+                all_ok = all_ok && ok;
+            }
+            if (__builtin_expect(!all_ok, 0)) {  // rare: these outputs exactly in int64
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    int lv[L];
+#pragma unroll
+                    for (int l = 0; l < L; ++l) lv[l] = acc[l][4 * q + i];
+                    v[i] = round_to_float_rare(combine_levels<L>(lv), er[4 * q + i] + ec);
+                }
+            }
+            if (col < N) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (rbase + 8 * q + i < M)
+                        __builtin_nontemporal_store(v[i], &cp[(size_t)(8 * q + i) * ldc]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto step = [&](v4i (&buf)[S], int it) RG_INLINE {
+        if (ks == 0) {
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[l][e] = 0;
+        }
+        v4i fa[S];
+#pragma unroll
+        for (int p = 0; p < S; ++p) fa[p] = band[ks * S + p][lane];
+#pragma unroll
+        for (int p = 0; p < S; ++p)
+#pragma unroll
+            for (int q = 0; q < S; ++q)
+                acc[p + q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[p], buf[q], acc[p + q], 0, 0, 0);
+        if (it + D < total) fetch(buf);
+        if (++ks == nkp) {
+            epilogue();
+            ks = 0;
+            ++jt;
+            if (jt < my_tiles) ec = eB[tile_of(jt) * 32 + (lane & 31)];
+        }
+    };
+    for (int it = 0; it < total; it += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (it + d < total) step(bq[d], it + d);
+    }
+#endif
+}
+
 // The definition, as plainly as possible: one thread per output, int64 sum of X * Y over
 // this part's share of k. Always writes an int64 partial.
 __global__ void __launch_bounds__(256)
@@ -772,6 +977,35 @@ void launch_contract_small(const Layout& L, const float* A, const float* B, floa
         default: break;
     }
 #undef RG_SMALL
+}
+
+void launch_contract_band(const Layout& L, const float* A, long long lda, const int8_t* qb,
+                          const int* eb, float* C, long long ldc, hipStream_t stream) {
+    // 16-byte loads for rows that start 16-byte aligned with K % 4 == 0
+    const int vec_a = (reinterpret_cast<uintptr_t>(A) & 15) == 0 && lda % 4 == 0 && L.K % 4 == 0;
+    const int nkp = (L.K + PANEL_K - 1) / PANEL_K;
+    const int nsl = (nkp * 64 + BAND_THREADS - 1) / BAND_THREADS;  // slots per thread, <= 4
+    const int qb_bytes = (int)((size_t)L.Np * L.Kp * L.S);  // < 2^31 (plan_layout)
+    const unsigned blocks = (unsigned)((L.Mp / 32) * L.band_groups);
+#define RG_BAND(SS, NS)                                                                         \
+    contract_band<SS, NS><<<blocks, BAND_THREADS, 0, stream>>>(A, lda, vec_a, qb, qb_bytes, eb,  \
+                                                              C, ldc, L.M, L.N, L.K, L.Kp,      \
+                                                              L.band_w, L.band_groups)
+#define RG_BAND_S(SS)                       \
+    switch (nsl) {                          \
+        case 1: RG_BAND(SS, 1); break;      \
+        case 2: RG_BAND(SS, 2); break;      \
+        case 3: RG_BAND(SS, 3); break;      \
+        default: RG_BAND(SS, 4); break;     \
+    }
+    switch (L.S) {
+        case 1: RG_BAND_S(1); break;
+        case 2: RG_BAND_S(2); break;
+        case 3: RG_BAND_S(3); break;
+        default: break;
+    }
+#undef RG_BAND_S
+#undef RG_BAND
 }
 
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,

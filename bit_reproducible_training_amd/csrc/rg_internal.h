@@ -87,6 +87,12 @@ constexpr int STEP_K = 64;  // k consumed per pipeline stage of the contraction
 constexpr int SMALL_MAX_K = 512;
 // Threads of a block of the one-launch small-shape kernel (one block per 32x32 tile of C).
 constexpr int SMALL_THREADS = 1024;
+// Band kernel (contract_band): longest K whose digit panels of a 32-row band of op(A) it keeps in
+// LDS (32 k panels x S KiB), threads per block, and k panels of op(B) each wavefront has in
+// flight.
+constexpr int BAND_MAX_K = 1024;
+constexpr int BAND_THREADS = 512;
+constexpr int BAND_DEPTH = 3;
 
 // Which output tile a contraction block computes. The hardware deals a launch's workgroups to
 // the 8 XCDs in turn (linear workgroup id mod 8), and each XCD has its own L2. The block at
@@ -136,6 +142,9 @@ struct Layout {
     int Mp, Np, Kp;     // padded sizes: Mp, Np multiples of the block tile, Kp of STEP_K
     int ti, tj;         // MFMA block tile = (64*ti) x (64*tj); 0 for REFERENCE and small
     bool small;         // one launch of contract_small (32x32 tiles, no workspace use)
+    int band_w;         // > 0: contract_band, blocks of 32 rows x band_w columns (op(B) sliced
+                        // first; op(A)'s digits never in the workspace); 0 otherwise
+    int band_groups;    // column groups of the band kernel (Np = band_groups * band_w)
     int split;          // split-K parts
     int xcd_chunk;      // contraction block order (xcd_order): blocks resident per XCD, or 0
     int group_m;        // tile rows per group of the block order (block_tile)
@@ -355,6 +364,10 @@ void launch_contract_mfma(const Layout& L, const int8_t* qa, const int8_t* qb, c
 // Whole GEMM (or batch) in one launch, for a layout with L.small.
 void launch_contract_small(const Layout& L, const float* A, const float* B, float* C,
                            const GemmAddressing& addr, hipStream_t stream);
+// Slicing of op(A), contraction and rounding in one launch, for a layout with L.band_w > 0
+// (op(B)'s digit panels qb and exponents eb already in the workspace).
+void launch_contract_band(const Layout& L, const float* A, long long lda, const int8_t* qb,
+                          const int* eb, float* C, long long ldc, hipStream_t stream);
 void launch_contract_reference(const Layout& L, const int32_t* xa, const int32_t* xb,
                                int64_t* partial, hipStream_t stream);
 void launch_reduce_round(const Layout& L, const int64_t* partial, const int* ea, const int* eb,

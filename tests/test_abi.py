@@ -148,11 +148,11 @@ def test_default_plan_follows_the_cost_model():
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 192, 1)
     p, _ = _plan(1024, 1024, 65536)       # 64 tiles of 128x128, 1024 stages
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 4)
-    p, _ = _plan(8192, 768, 768, trans_b=True)    # 1536 tiles of 64x64 = 3 waves of 512
+    p, _ = _plan(8192, 768, 768, trans_b=True, tile_m=64, tile_n=64)  # 3 waves of 512 tiles
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 1)
     p, _ = _plan(1024, 768, 768, trans_b=True)    # one wave either way: no split traffic
     assert p.split_k == 1
-    p, _ = _plan(8192, 2304, 768, trans_b=True)   # 12 stages: 64x64's short prologue wins
+    p, _ = _plan(8192, 768, 3072, tile_m=64, tile_n=64)   # a pinned tile is kept
     assert (p.tile_m, p.tile_n, p.split_k) == (64, 64, 1)
     p, _ = _plan(50257, 768, 8192, trans_a=True)  # LM-head weight gradient
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
@@ -164,6 +164,35 @@ def test_default_plan_follows_the_cost_model():
     assert (p.tile_m, p.tile_n, p.split_k) == (128, 128, 1)
     p, _ = _plan(8192, 768, 3072, slices=2)   # the twelve-wavefront tiles exist at S = 3 only
     assert (p.tile_m, p.tile_n) in ((128, 128), (64, 64))
+
+
+def test_band_kernel_plans():
+    """op(A) read along rows with K <= 1024 over many rows takes the band kernel (plan 32 x W:
+    blocks of 32 rows of op(A) by W columns) where its cost model beats the best tile plan plus
+    op(A)'s slicing: the GPT-2 forward and input-gradient GEMMs at N = 768 and 2304 (measured on
+    MI355X: 3-18% faster than the 64x64 tiles), not N = 3072 (the 128x128 tiles 2% faster), not
+    a transposed op(A), K past 1024, a batch, a pinned tile or split. A pinned 32 x W tile (W >= 64,
+    a multiple of 32) asks for it; the workspace then holds op(B)'s regions only."""
+    for tb in (True, False):
+        p, _ = _plan(8192, 768, 768, trans_b=tb)      # attn_proj forward (NT) and dX (NN)
+        assert (p.tile_m, p.tile_n, p.split_k) == (32, 768, 1)
+    p, _ = _plan(8192, 2304, 768, trans_b=True)       # qkv forward
+    assert (p.tile_m, p.tile_n, p.split_k) == (32, 2304, 1)
+    p, _ = _plan(8192, 3072, 768, trans_b=True)       # mlp_fc forward
+    assert (p.tile_m, p.tile_n) == (128, 128)
+    for kw in (dict(trans_a=True), dict(split_k=2), dict(tile_m=64, tile_n=64),
+               dict(algo=rg.Algo.Tiled)):
+        p, _ = _plan(8192, 768, 768, **kw)
+        assert p.tile_m != 32, kw
+    p, _ = _plan(8192, 768, 1056)                     # K past the band's LDS panels
+    assert p.tile_m != 32
+    p, info = _plan(97, 70, 203, tile_m=32, tile_n=64)
+    assert (p.tile_m, p.tile_n, p.split_k) == (32, 64, 1)
+    assert info.Np == 128 and info.qa == info.qb == 0   # two column groups; no op(A) regions
+    p, _ = _plan(97, 70, 203, tile_m=32, tile_n=64, trans_a=True)   # not for a transposed op(A)
+    assert (p.tile_m, p.tile_n) != (32, 64)
+    p, _ = _plan(97, 70, 203, tile_m=32, tile_n=48)   # W must be a multiple of 32
+    assert (p.tile_m, p.tile_n) != (32, 48)
 
 
 def test_small_shapes_take_the_one_launch_kernel():

@@ -32,9 +32,11 @@ def _order(M, N, K, batch=1, num_cus=CUS, **kw):
 
 SHAPES = [
     (4096, 4096, 4096, {}),
-    (8192, 768, 768, {"trans_b": True}),
+    # (the GPT-2 K = 768 forward shapes take the band kernel by default, which has no tile
+    # order: their 64x64 tile plans pinned)
+    (8192, 768, 768, {"trans_b": True, "tile_m": 64, "tile_n": 64}),
     (8192, 768, 3072, {}),
-    (8192, 2304, 768, {"trans_b": True}),
+    (8192, 2304, 768, {"trans_b": True, "tile_m": 64, "tile_n": 64}),
     (2304, 768, 8192, {"trans_a": True}),
     (768, 768, 8192, {"trans_a": True}),
     (1024, 1024, 65536, {}),
