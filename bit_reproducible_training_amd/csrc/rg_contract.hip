@@ -629,7 +629,7 @@ contract_small(SmallOperand a, SmallOperand b, float* __restrict__ C, int K, lon
 // The loads of op(B) go through a buffer resource over its digit region, so an offset out of
 // the region would read zeros instead of faulting.
 template <int S, int NSL>
-__global__ void __launch_bounds__(BAND_THREADS, 2)
+__global__ void __launch_bounds__(BAND_THREADS, BAND_THREADS / 256)
 contract_band(const float* __restrict__ A, long long lda, int vec_a, const int8_t* __restrict__ QB,
               int qb_bytes, const int* __restrict__ eB, float* __restrict__ C, long long ldc,
               int M, int N, int K, int Kp_ws, int W, int groups) {
@@ -648,9 +648,10 @@ contract_band(const float* __restrict__ A, long long lda, int vec_a, const int8_
     const int npk_ws = Kp_ws / PANEL_K;           // k panels per 32-column panel of QB
     const int ntile = W / 32;
     const int tc0 = g * ntile;                    // first column tile of the block
-    const int my_tiles = ntile > wave ? (ntile - wave + 7) / 8 : 0;
+    constexpr int NW = BAND_THREADS / 64;        // wavefronts per block
+    const int my_tiles = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;
     const int total = my_tiles * nkp;             // (tile, k panel) steps of this wavefront
-    auto tile_of = [&](int j) RG_INLINE { return tc0 + wave + 8 * j; };
+    auto tile_of = [&](int j) RG_INLINE { return tc0 + wave + NW * j; };
 
     // op(B)'s panels of this wavefront's steps, fetched D steps ahead, in step order.
     const __amdgpu_buffer_rsrc_t rsrc =

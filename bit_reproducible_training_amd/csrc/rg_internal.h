@@ -91,8 +91,8 @@ constexpr int SMALL_THREADS = 1024;
 // LDS (32 k panels x S KiB), threads per block, and k panels of op(B) each wavefront has in
 // flight.
 constexpr int BAND_MAX_K = 1024;
-constexpr int BAND_THREADS = 512;
-constexpr int BAND_DEPTH = 3;
+constexpr int BAND_THREADS = 768;
+constexpr int BAND_DEPTH = 2;
 
 // Which output tile a contraction block computes. The hardware deals a launch's workgroups to
 // the 8 XCDs in turn (linear workgroup id mod 8), and each XCD has its own L2. The block at

@@ -38,6 +38,8 @@ enum {
  * tile_m/tile_n: the reference ignores them; here a pair naming an MFMA block tile
  * (128x128, 128x64, 64x128, 64x64, and at slices = 3 64x192 or 192x64) forces that tile;
  * 32x32 asks for the one-launch small-GEMM kernel (K <= 512, default split_k, plain GEMMs);
+ * 32xW (W >= 64, a multiple of 32) asks for the band kernel with blocks of 32 rows of op(A)
+ * by W columns (op(A) not transposed, K <= 1024, default split_k, plain GEMMs);
  * anything else lets the planner choose. tile_k is ignored. */
 typedef struct rg_config {
     int split_k;  /* >= 1; raised when needed for exact int32 sums, and from the default 1
@@ -56,7 +58,7 @@ typedef struct rg_plan {
     int algo;               /* resolved, never RG_ALGO_AUTO */
     int split_k;            /* effective split count */
     size_t workspace_bytes; /* size needed by rg_gemm_fp32_ws */
-    int tile_m;             /* block tile rows (MFMA algorithms; 32: one-launch kernel), 0 for REFERENCE */
+    int tile_m;             /* block tile rows (MFMA algorithms; 32: one-launch or band kernel), 0 for REFERENCE */
     int tile_n;             /* block tile columns */
 } rg_plan;
 

@@ -33,8 +33,9 @@ struct Config {
     int split_k = 1;        // K-parts summed in int64; the planner may use more (int32 chunk
                             // limit, or to fill the GPU); never changes a bit of C
     int tile_m = 16;        // 64 or 128 (with tile_n; 64x192 / 192x64 at S = 3) pins that MFMA
-    int tile_n = 16;        //   block tile, 32x32 the one-launch kernel for K <= 512; other
-                            //   values leave the choice to the planner
+    int tile_n = 16;        //   block tile, 32x32 the one-launch kernel for K <= 512, 32xW
+                            //   (W >= 64) the band kernel for K <= 1024; other values leave
+                            //   the choice to the planner
     int tile_k = 32;        // not used
     Algo algo = Algo::Auto;
     int slices = 3;         // S in 1..MAX_SLICES: inputs rounded to 7*S-bit integers
