@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import bit_reproducible_training_amd as rg
-from gpu_util import bits, note, run, to_dev
+from gpu_util import bits, decode_digits, note, run, to_dev
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -44,9 +44,16 @@ def test_band_shapes_against_the_oracle(torch_gpu, M, N, K, W, tb):
     A, B = _inputs(M, N, K, tb, M * 3 + N * 5 + K + tb)
     want = O.cpu_gemm(A, B, M, N, K, 0, tb, 3).view(np.uint32)
     note("band M=%d N=%d K=%d W=%d tb=%d" % (M, N, K, W, tb))
-    C, plan, _ = run(torch, A, B, M, N, K, _band_cfg(W, 3, tb))
+    C, plan, ws = run(torch, A, B, M, N, K, _band_cfg(W, 3, tb))
     assert (plan.tile_m, plan.tile_n, plan.split_k) == (32, W, 1)
     assert np.array_equal(bits(C), want), (M, N, K, W, tb)
+    # op(B)'s digit panels and exponents, sliced into the workspace by the launch before
+    info = rg.workspace_layout(M, N, K, _band_cfg(W, 3, tb))
+    _, Y, _, eB = O.quantize(A, B, M, N, K, 0, tb, 3)
+    w = ws.cpu().numpy()
+    _, Yg = decode_digits(w, info.qb, info.Np, info.Kp, 3)
+    assert np.array_equal(Yg[:N, :K], Y) and not Yg[N:, :K].any()
+    assert np.array_equal(w[info.eb:info.eb + 4 * info.Np].view(np.int32)[:N], eB)
 
 
 @pytest.mark.parametrize("S", [1, 2])
