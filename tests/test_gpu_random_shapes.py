@@ -46,3 +46,38 @@ def test_random_shapes_and_plans(torch_gpu, chunk):
         note("random M=%d N=%d K=%d ta=%d tb=%d S=%d %s %s seed=%d" % (M, N, K, ta, tb, S, plan, dist, seed))
         C, got_plan, _ = run(torch, As.ravel(), Bs.ravel(), M, N, K, cfg)
         assert np.array_equal(bits(C), want), (M, N, K, ta, tb, S, plan, dist, seed, got_plan)
+
+
+# The band kernel pinned (32 x W): ragged rows, columns and K up to its 1024, every slice count,
+# both transposes of op(B) (a transposed op(A) falls back to the planner's choice).
+BAND_PLANS = [dict(tile_m=32, tile_n=64), dict(tile_m=32, tile_n=96), dict(tile_m=32, tile_n=256),
+              dict(tile_m=32, tile_n=160)]
+
+
+def _band_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M = int(rng.integers(1, 700))
+        N = int(rng.integers(1, 500))
+        K = int(rng.choice([rng.integers(1, 64), rng.integers(64, 1025)]))
+        out.append((M, N, K, int(rng.integers(0, 8) == 0), int(rng.integers(0, 2)),
+                    int(rng.integers(1, 4)), BAND_PLANS[i % len(BAND_PLANS)],
+                    rng.choice(O.HASH_DISTS), int(rng.integers(1, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_random_shapes_band_plans(torch_gpu, chunk):
+    torch = torch_gpu
+    for M, N, K, ta, tb, S, plan, dist, seed in _band_cases(48, 2000 + chunk):
+        A, B = O.gen_hash_inputs(M, N, K, seed, dist)
+        want = O.cpu_gemm(A, B, M, N, K, 0, 0, S).view(np.uint32)
+        As = np.ascontiguousarray(A.T) if ta else A
+        Bs = np.ascontiguousarray(B.T) if tb else B
+        cfg = rg.Config(slices=S, trans_a=bool(ta), trans_b=bool(tb), **plan)
+        note("random band M=%d N=%d K=%d ta=%d tb=%d S=%d %s %s seed=%d" % (M, N, K, ta, tb, S, plan, dist, seed))
+        C, got_plan, _ = run(torch, As.ravel(), Bs.ravel(), M, N, K, cfg)
+        if not ta:
+            assert (got_plan.tile_m, got_plan.tile_n) == (32, plan["tile_n"])
+        assert np.array_equal(bits(C), want), (M, N, K, ta, tb, S, plan, dist, seed, got_plan)
