@@ -46,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671613952, ("rg_contract.hip", "rg_internal.h"),
-                 "43b8b7bf36eeb805cfe73642e4e86e8137f503e2687bcee8cfbbfc89184c952c"),
-    "slicing": (235628237, ("rg_slice.hip", "rg_internal.h"),
-                "96deb96458e8f961534dcf976ce79d8d80b30d579f9c37ad09440118a5a2ff3b"),
+                 "711faf79ada209e89df94280c7e2b9424900e28dfc5ad0a718dd763dfd30ace6"),
+    "slicing": (235627008, ("rg_slice.hip", "rg_internal.h"),
+                "4365ba3218111bc0089ac439b2a830e84ea00b5be37b078c5079c1d842c68b00"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 

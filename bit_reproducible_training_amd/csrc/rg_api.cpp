@@ -763,10 +763,6 @@ int rg_test_pslice_placement(int M, int N, int K, const rg_config* cfg, int num_
         d.batch = L.batch;
         d.strided = op.strided ? 1 : 0;
         rg::pslice_grid(d);
-        if (d.ps_dev) {  // spread over every XCD by design, exchanging through memory
-            *blocks += d.ps_blocks;
-            continue;
-        }
         const long long panels = (long long)d.batch * (d.Rp / (d.strided ? rg::PANEL_ROWS : 8));
         std::vector<int> xcd((size_t)panels, -1);
         for (long long blk = 0; blk < d.ps_blocks; ++blk) {

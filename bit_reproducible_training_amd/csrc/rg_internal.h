@@ -219,9 +219,9 @@ struct SliceDesc {
     int ps_parts;
     int spin_limit;
     long long ps_blocks;
-    // Device-scope exchange (column access with more than PS_MAX_PARTS parts): a panel's parts
-    // run on every XCD and exchange their maxima through memory instead of one XCD's L2.
-    int ps_dev;
+    // k panels per wavefront of a column-access operand (pslice_kpw: PS_KPW, or PS_KPW_WIDE
+    // for K past 32768).
+    int ps_kpw;
     // Null, or one flag per stacked row (batch * Rp): a row whose flag is non-zero takes
     // exponent 0, the exponent of a maximum that a NaN wins (the convolution's window and
     // position maxima; the maxima computed here skip NaN).
@@ -252,31 +252,39 @@ void launch_onepass(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use
                     hipStream_t stream);
 
 // One-read slicing of an operand whose padded K is past the one-pass limit: a block holds a
-// 32-row panel of op(X) (column access: 32 columns of the stored matrix) over PS_NPB k panels,
-// or a strip of 8 rows (row access) over PS_ROW_NPB k panels, in registers, and the ps_parts
-// blocks of a panel or strip exchange their partial maxima.
+// 32-row panel of op(X) (column access: 32 columns of the stored matrix) over PS_WAVES * kpw k
+// panels, or a strip of 8 rows (row access) over PS_ROW_NPB k panels, in registers, and the
+// ps_parts blocks of a panel or strip exchange their partial maxima.
 constexpr int PS_WAVES = 8;
 constexpr int PS_KPW = 4;                        // k panels per wavefront (column access)
 constexpr int PS_NPB = PS_WAVES * PS_KPW;        // k panels per block (column access)
 constexpr int PS_ROW_NF4 = 16;                   // k panels per wavefront (row access)
 constexpr int PS_ROW_NPB = PS_WAVES * PS_ROW_NF4;
-__host__ __device__ inline int pslice_parts(bool strided, int Kp) {
-    const int npb = strided ? PS_NPB : PS_ROW_NPB;
-    return (Kp / PANEL_K + npb - 1) / npb;
-}
 // At most this many parts per panel exchanging through one XCD's L2: the parts of a panel wait
 // for each other, so they must be resident together on that XCD (64 slots of these blocks per
 // XCD at S = 3); with 64 parts they needed every slot at once and waited out their bound
 // (measured: 1024x1024x65536 NN), with 32 they did not.
 constexpr int PS_MAX_PARTS = 32;
-// Column-access operands with more parts (K up to 65536) spread each panel's parts over all
-// XCDs (eight per XCD at 64 parts) and exchange through memory at device scope (ps_dev):
-// 1024x1024x65536 NN slicing 0.259 -> 0.229 ms against the two passes. Longer operands (column
-// access past K = 65536, row access past 131072) keep the two passes.
-constexpr int PS_MAX_PARTS_DEV = 64;
+// Column-access operands that would need more parts (K past 32768) take parts twice as long:
+// PS_KPW_WIDE k panels per wavefront, so K up to 65536 is at most 32 parts, which still run
+// on one XCD and exchange through its L2 (the wide form: 173 registers, one block per compute
+// unit, 32 per XCD). Against 64 parts spread over every XCD exchanging through memory,
+// 1024x1024x65536 slicing took 0.259 -> 0.222 ms with both operands column-access (TN) and
+// 0.229 -> 0.224 ms with B alone (NN), on one box. Longer operands (column access past
+// K = 65536, row access past 131072) keep the two passes.
+constexpr int PS_KPW_WIDE = 8;
+// k panels per wavefront of a column-access operand's one read (0 for row access).
+__host__ __device__ inline int pslice_kpw(bool strided, int Kp) {
+    if (!strided) return 0;
+    return (Kp / PANEL_K + PS_NPB - 1) / PS_NPB > PS_MAX_PARTS ? PS_KPW_WIDE : PS_KPW;
+}
+__host__ __device__ inline int pslice_parts(bool strided, int Kp) {
+    const int npb = strided ? PS_WAVES * pslice_kpw(strided, Kp) : PS_ROW_NPB;
+    return (Kp / PANEL_K + npb - 1) / npb;
+}
 __host__ __device__ inline bool pslice_route(bool strided, int Kp) {
     return Kp > (strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K) &&
-           pslice_parts(strided, Kp) <= (strided ? PS_MAX_PARTS_DEV : PS_MAX_PARTS);
+           pslice_parts(strided, Kp) <= PS_MAX_PARTS;
 }
 // Polls of a block's wait for the other parts of its panel before it reads their k ranges
 // itself (rg_test_set_spin_limit sets it; 0: no exchange, every block reads its panel's whole K
@@ -293,8 +301,8 @@ void pslice_grid(SliceDesc& d);
 // runs on XCD blk % 8, and each XCD takes a contiguous range of ps_blocks / 8 units, which
 // pslice_grid makes a whole number of panels (or strips): the parts of a panel, which exchange
 // their maxima through the XCD's L2, then all run on one XCD.
-__host__ __device__ inline long long pslice_unit(long long blk, long long ps_blocks, bool dev = false) {
-    return dev ? blk : (blk & 7) * (ps_blocks / 8) + (blk >> 3);
+__host__ __device__ inline long long pslice_unit(long long blk, long long ps_blocks) {
+    return (blk & 7) * (ps_blocks / 8) + (blk >> 3);
 }
 // The partial-maximum slots the one read of d waits on.
 MarkRange pslice_slots(const SliceDesc& d);

@@ -585,7 +585,7 @@ __device__ __forceinline__ float4 im2col_values(const Im2col& g, const float* xn
 // NT: row-access loads are non-temporal (the fp32 values are read once and need not stay in
 // the caches), used where another operand is read twice in the same GEMM.
 template <int S, int NF4, bool WS = false, bool G = false, bool NT = false>
-__device__ void slice_onepass(const SliceDesc& d, long long blk) {
+__device__ __forceinline__ void slice_onepass(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][8];
     __shared__ int sse[8];
     __shared__ float tr[8][8][33];
@@ -902,8 +902,8 @@ void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hi
 
 // One read of a column-access operand past the one-pass limit (element (r, k) of item b at
 // src[b*bstride + k*ld + r]). Block (rp, part) owns the 32-row panel rp of op(X) (32
-// neighbouring columns of the stored matrix) over the k panels [part*PS_NPB, (part+1)*PS_NPB):
-// wavefront w takes PS_KPW of them, lane L column L % 32 and the 16 k of half L / 32 of each, as
+// neighbouring columns of the stored matrix) over the k panels [part*8*KPW, (part+1)*8*KPW):
+// wavefront w takes KPW of them, lane L column L % 32 and the 16 k of half L / 32 of each, as
 // scalar loads (each load instruction reads two 128-byte k-row segments), and keeps them in
 // registers. The panel's row maxima need every part: each block publishes its 32 partial maxima
 // in its slots pmax[part][rows] and waits until the other parts' slots of the panel hold values
@@ -925,11 +925,8 @@ void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hi
 // XCD's whole L2 while the launch's other blocks fill it with digits. A block whose parts ran on
 // another XCD can only see PM_EMPTY or this call's maxima (the slots were marked by an earlier
 // launch, whose writes the launch boundary made visible everywhere), so at worst it takes the
-// fallback: placement never changes a bit. A column-access operand with more parts than one
-// XCD holds at once (ps_dev) runs its panels' parts in the plain order instead, i.e. spread over
-// every XCD, and exchanges at device scope: the slot store is written through to memory and the
-// polls miss the L2 (scope bit sc1 on those instructions only; no cache-wide write-back or
-// invalidate).
+// fallback: placement never changes a bit. KPW = PS_KPW_WIDE (K past 32768) doubles each
+// part's k range so that a panel still has at most 32 parts, which one XCD holds at once.
 // Eight slot words read past the L1 with one wait: a poll costs one round trip per eight parts
 // (the LM head's weight gradient, 8 parts: slicing 0.605 -> 0.595 ms against four per wait,
 // 0.65 ms with one).
@@ -949,35 +946,10 @@ __device__ __forceinline__ void load8_bypass_l1(const unsigned* const (&p)[8], u
         : "memory");
 }
 
-// Device scope (sc1): a store written through to memory and loads that miss the XCD's L2, for
-// parts that run on different XCDs; no cache-wide write-back or invalidate.
-__device__ __forceinline__ void load8_device(const unsigned* const (&p)[8], unsigned (&v)[8]) {
-    asm volatile(
-        "global_load_dword %0, %8, off sc1\n\t"
-        "global_load_dword %1, %9, off sc1\n\t"
-        "global_load_dword %2, %10, off sc1\n\t"
-        "global_load_dword %3, %11, off sc1\n\t"
-        "global_load_dword %4, %12, off sc1\n\t"
-        "global_load_dword %5, %13, off sc1\n\t"
-        "global_load_dword %6, %14, off sc1\n\t"
-        "global_load_dword %7, %15, off sc1\n\t"
-        "s_waitcnt vmcnt(0)"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
-        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7])
-        : "memory");
-}
-__device__ __forceinline__ void store_device(unsigned* p, unsigned v) {
-    asm volatile("global_store_dword %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
-}
-
 __device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride, int part, int parts,
-                                               int spin_limit, int lane, int nl, float* mm,
-                                               bool dev = false) {
+                                               int spin_limit, int lane, int nl, float* mm) {
     if (spin_limit <= 0) return false;
-    if (lane < nl) {
-        if (dev) store_device(pm + (size_t)part * part_stride, __float_as_uint(*mm));
-        else pm[(size_t)part * part_stride] = __float_as_uint(*mm);
-    }
+    if (lane < nl) pm[(size_t)part * part_stride] = __float_as_uint(*mm);
     for (int n = 0;; ++n) {
         float m = *mm;
         bool seen = true;
@@ -988,8 +960,7 @@ __device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride,
 #pragma unroll
                 for (int j = 0; j < 8; ++j) q[j] = pm + (size_t)min(p0 + j, parts - 1) * part_stride;
                 unsigned v[8];
-                if (dev) load8_device(q, v);
-                else load8_bypass_l1(q, v);
+                load8_bypass_l1(q, v);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     if (p0 + j >= parts || p0 + j == part) continue;
@@ -1006,8 +977,8 @@ __device__ __forceinline__ bool panel_exchange(unsigned* pm, size_t part_stride,
     }
 }
 
-template <int S>
-__device__ void pslice_cols(const SliceDesc& d, long long blk) {
+template <int S, int KPW>
+__device__ __forceinline__ void pslice_cols(const SliceDesc& d, long long blk) {
     __shared__ float smax[16][32];
     __shared__ float sfin[32];
     __shared__ int sse[32];
@@ -1015,7 +986,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
     const int npk = d.Kp / PANEL_K;
     const int parts = d.ps_parts;
     const long long rpanels = (long long)d.batch * (d.Rp / PANEL_ROWS);
-    const long long lin = pslice_unit(blk, d.ps_blocks, d.ps_dev != 0);
+    const long long lin = pslice_unit(blk, d.ps_blocks);
     if (lin >= rpanels * parts) return;  // padding block (whole block)
     const int rp = (int)(lin / parts), part = (int)(lin - (long long)rp * parts);
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -1026,18 +997,18 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
     const int q = rp * PANEL_ROWS + (lane & 31);
     const float* colp = d.src + (size_t)item * d.bstride + r;
     const bool live = r < d.R;
-    const int kp0 = part * PS_NPB + wv * PS_KPW;
-    float x[PS_KPW][16];
-    if (live && (kp0 + PS_KPW) * PANEL_K <= d.K) {  // every value of this wavefront inside K
+    const int kp0 = part * (PS_WAVES * KPW) + wv * KPW;
+    float x[KPW][16];
+    if (live && (kp0 + KPW) * PANEL_K <= d.K) {  // every value of this wavefront inside K
 #pragma unroll
-        for (int i = 0; i < PS_KPW; ++i) {
+        for (int i = 0; i < KPW; ++i) {
             const float* p = colp + (size_t)((kp0 + i) * PANEL_K + 16 * h) * d.ld;
 #pragma unroll
             for (int j = 0; j < 16; ++j) x[i][j] = p[(size_t)j * d.ld];
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < PS_KPW; ++i) {
+        for (int i = 0; i < KPW; ++i) {
             const int k0 = (kp0 + i) * PANEL_K + 16 * h;
 #pragma unroll
             for (int j = 0; j < 16; ++j)
@@ -1046,7 +1017,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
     }
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < PS_KPW; ++i)
+    for (int i = 0; i < KPW; ++i)
 #pragma unroll
         for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(x[i][j]));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
@@ -1062,7 +1033,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
         int ok = 1;
         if (parts > 1) {
             unsigned* pm = reinterpret_cast<unsigned*>(d.pmax) + rp * PANEL_ROWS + (lane & 31);
-            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, 32, &mm, d.ps_dev != 0) ? 1 : 0;
+            ok = panel_exchange(pm, rows_total, part, parts, d.spin_limit, lane, 32, &mm) ? 1 : 0;
         }
         if (lane < 32) sfin[lane] = mm;
         if (lane == 0) sok = ok;
@@ -1094,7 +1065,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
     __syncthreads();
     const RowScale rs = row_scale<S>(sse[lane & 31]);
 #pragma unroll
-    for (int i = 0; i < PS_KPW; ++i)
+    for (int i = 0; i < KPW; ++i)
         if (kp0 + i < npk) emit_panel<S, false>(d, x[i], rs, rp, kp0 + i, q, h, lane);
 }
 
@@ -1104,7 +1075,7 @@ __device__ void pslice_cols(const SliceDesc& d, long long blk) {
 // strip (wavefront w: PS_ROW_NF4 k panels, lane L: row L/8 and k 4*(L%8)..+3 of each panel, 16-byte
 // loads), and exchanges its 8 partial maxima with the strip's other parts as pslice_cols does.
 template <int S>
-__device__ void pslice_rows(const SliceDesc& d, long long blk) {
+__device__ __forceinline__ void pslice_rows(const SliceDesc& d, long long blk) {
     __shared__ float smax[8][8];
     __shared__ float sfin[8];
     __shared__ int sse[8];
@@ -1200,17 +1171,19 @@ __device__ void pslice_rows(const SliceDesc& d, long long blk) {
     }
 }
 
-template <int S>
+// WIDE: the launch's column-access operands take PS_KPW_WIDE k panels per wavefront (instantiated
+// apart, so that the common form keeps its register budget).
+template <int S, bool WIDE>
 __device__ __forceinline__ void pslice_block(const SliceDesc& d, long long blk) {
-    if (d.strided) pslice_cols<S>(d, blk);
+    if (d.strided) pslice_cols<S, WIDE ? PS_KPW_WIDE : PS_KPW>(d, blk);
     else pslice_rows<S>(d, blk);
 }
 
-template <int S>
-__global__ void __launch_bounds__(64 * PS_WAVES) pslice_kernel(SliceDesc a, SliceDesc b) {
+template <int S, bool WIDE>
+__global__ void __launch_bounds__(64 * PS_WAVES, WIDE ? 2 : 4) pslice_kernel(SliceDesc a, SliceDesc b) {
     const long long blk = blockIdx.x;
-    if (blk < a.ps_blocks) pslice_block<S>(a, blk);
-    else pslice_block<S>(b, blk - a.ps_blocks);
+    if (blk < a.ps_blocks) pslice_block<S, WIDE>(a, blk);
+    else pslice_block<S, WIDE>(b, blk - a.ps_blocks);
 }
 
 // The one read of operand `two` and the one pass of operand `one` in one launch (two's slots
@@ -1219,7 +1192,7 @@ __global__ void __launch_bounds__(64 * PS_WAVES) pslice_kernel(SliceDesc a, Slic
 template <int S, int NF4>
 __global__ void __launch_bounds__(512) onepass_pslice_kernel(SliceDesc one, SliceDesc two) {
     const long long blk = blockIdx.x;
-    if (blk < two.ps_blocks) pslice_block<S>(two, blk);
+    if (blk < two.ps_blocks) pslice_block<S, false>(two, blk);  // K <= 4096: never wide
     else slice_onepass<S, NF4>(one, blk - two.ps_blocks);
 }
 
@@ -1228,7 +1201,7 @@ __global__ void __launch_bounds__(512) onepass_pslice_kernel(SliceDesc one, Slic
 template <int S>
 __global__ void __launch_bounds__(512) pslice_absmax_kernel(SliceDesc ps, SliceDesc two) {
     const long long blk = blockIdx.x;
-    if (blk < ps.ps_blocks) pslice_block<S>(ps, blk);
+    if (blk < ps.ps_blocks) pslice_block<S, false>(ps, blk);  // a wide ps runs on its own
     else if (two.strided) absmax_cols<8>(two, blk - ps.ps_blocks);
     else absmax_rows<8>(two, blk - ps.ps_blocks);
 }
@@ -1254,11 +1227,7 @@ void set_slice_spin_limit(int polls) { g_spin_limit = polls < 0 ? 0 : polls; }
 
 void pslice_grid(SliceDesc& d) {
     d.ps_parts = pslice_parts(d.strided != 0, d.Kp);
-    d.ps_dev = d.strided && d.ps_parts > PS_MAX_PARTS ? 1 : 0;
-    if (d.ps_dev) {  // plain order: consecutive parts of a panel on consecutive XCDs
-        d.ps_blocks = ((long long)d.batch * (d.Rp / PANEL_ROWS) * d.ps_parts + 7) / 8 * 8;
-        return;
-    }
+    d.ps_kpw = pslice_kpw(d.strided != 0, d.Kp);
     // Whole panels (strips) per XCD: a panel's parts must not be split between two XCDs, whose
     // L2s do not see each other's slots (they would wait out their bound and re-read K).
     const long long panels = (long long)d.batch * (d.Rp / (d.strided ? PANEL_ROWS : 8));
@@ -1281,11 +1250,24 @@ void launch_pslice(const SliceDesc& a, bool use_a, const SliceDesc& b, bool use_
     if (!use_b) y.ps_blocks = 0;
     const unsigned blocks = (unsigned)(x.ps_blocks + y.ps_blocks);
     if (blocks == 0) return;
-    switch (S) {
-        case 1: pslice_kernel<1><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y); break;
-        case 2: pslice_kernel<2><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y); break;
-        default: pslice_kernel<3><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y); break;
+    const bool wx = x.ps_blocks && x.ps_kpw == PS_KPW_WIDE, wy = y.ps_blocks && y.ps_kpw == PS_KPW_WIDE;
+    if (x.ps_blocks && y.ps_blocks && wx != wy) {
+        // The wide form holds half the waves per SIMD: the other operand takes a launch of its own.
+        launch_pslice(a, true, b, false, S, stream);
+        launch_pslice(a, false, b, true, S, stream);
+        return;
     }
+    const bool wide = wx || wy;
+#define RG_PS(SS, W) pslice_kernel<SS, W><<<blocks, 64 * PS_WAVES, 0, stream>>>(x, y)
+    switch (S * 2 + (wide ? 1 : 0)) {
+        case 2: RG_PS(1, false); break;
+        case 3: RG_PS(1, true); break;
+        case 4: RG_PS(2, false); break;
+        case 5: RG_PS(2, true); break;
+        case 7: RG_PS(3, true); break;
+        default: RG_PS(3, false); break;
+    }
+#undef RG_PS
 }
 
 void launch_onepass_pslice(const SliceDesc& one, const SliceDesc& two, int S, hipStream_t stream) {
@@ -1310,11 +1292,17 @@ void launch_onepass_pslice(const SliceDesc& one, const SliceDesc& two, int S, hi
 }
 
 void launch_pslice_absmax(const SliceDesc& ps, const SliceDesc& two, int S, hipStream_t stream) {
-    const unsigned blocks = (unsigned)(ps.ps_blocks + absmax8_blocks(two));
+    SliceDesc x = ps;
+    if (ps.strided && ps.ps_kpw == PS_KPW_WIDE) {
+        // the wide form (half the waves per SIMD) on its own, then two's maxima
+        launch_pslice(ps, true, ps, false, S, stream);
+        x.ps_blocks = 0;
+    }
+    const unsigned blocks = (unsigned)(x.ps_blocks + absmax8_blocks(two));
     switch (S) {
-        case 1: pslice_absmax_kernel<1><<<blocks, 512, 0, stream>>>(ps, two); break;
-        case 2: pslice_absmax_kernel<2><<<blocks, 512, 0, stream>>>(ps, two); break;
-        default: pslice_absmax_kernel<3><<<blocks, 512, 0, stream>>>(ps, two); break;
+        case 1: pslice_absmax_kernel<1><<<blocks, 512, 0, stream>>>(x, two); break;
+        case 2: pslice_absmax_kernel<2><<<blocks, 512, 0, stream>>>(x, two); break;
+        default: pslice_absmax_kernel<3><<<blocks, 512, 0, stream>>>(x, two); break;
     }
 }
 

@@ -135,9 +135,8 @@ int rg_test_block_order(int M, int N, int K, const rg_config* cfg, int is_gfx950
  * arguments). *blocks receives the one-read blocks of both operands (0 when neither takes that
  * route) and *split_panels the number of row panels (strips of 8 rows for row access) whose
  * parts along K run on more than one XCD (workgroup i on XCD i mod 8); such parts cannot see
- * each other's partial maxima through their L2 and each waits out its bound. Operands whose
- * panels exchange at device scope (column access past 32 parts) are spread over the XCDs on
- * purpose and are not counted. Host only; 1 (invalid value) as rg_test_block_order. */
+ * each other's partial maxima through their L2 and each waits out its bound. Host only;
+ * 1 (invalid value) as rg_test_block_order. */
 int rg_test_pslice_placement(int M, int N, int K, const rg_config* cfg, int num_cus, int batch,
                              long long* blocks, long long* split_panels);
 

@@ -122,13 +122,16 @@ def test_resident_blocks_share_panels(M, N, K, kw):
 # panel counts that are and are not multiples of 8: the headline, the GPT-2 weight gradients,
 # the LM head's (1571 column panels of 8 parts), a ragged batch, and the convolution weight
 # gradients of the widened benchmark (LeNet conv2: 10000 windows, 150 and 16 columns; ResNet-like
-# 100352 windows is past the one-read limit and keeps two passes).
+# 100352 windows is past the one-read limit and keeps two passes), and column-access operands
+# past K = 32768, whose parts are twice as long (at most 32 per panel).
 PSLICE_SHAPES = [
     (4096, 4096, 4096, 1, {}),
     (768, 768, 8192, 1, {"trans_a": True}),
     (2304, 768, 8192, 1, {"trans_a": True}),
     (50257, 768, 8192, 1, {"trans_a": True}),
     (1024, 1024, 65536, 1, {}),
+    (1024, 1024, 65536, 1, {"trans_a": True}),
+    (300, 40, 40000, 1, {"trans_a": True, "trans_b": True}),
     (16, 150, 10000, 1, {"trans_a": True}),
     (6, 150, 5000, 1, {"trans_a": True}),
     (96, 40, 6000, 3, {"trans_b": True}),

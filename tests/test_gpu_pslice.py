@@ -23,10 +23,11 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 # Padded K from just past the column one-pass limit (3072) to several parts of 1024 k, and past
-# 32 parts (K > 32768), where a column-access operand's parts run on every XCD and exchange
-# their maxima at device scope.
+# 32 such parts (K > 32768), where a column-access operand's parts are twice as long (2048 k:
+# at most 32 parts, on one XCD), including the boundary K = 32768 / 32769.
 SHAPES = [(64, 100, 3076), (33, 200, 4096), (100, 33, 5000), (130, 70, 8193), (32, 32, 3073),
-          (70, 45, 4097), (24, 40, 12289), (9, 17, 20000), (40, 33, 40000), (20, 64, 65536)]
+          (70, 45, 4097), (24, 40, 12289), (9, 17, 20000), (40, 33, 40000), (20, 64, 65536),
+          (33, 40, 32768), (40, 20, 32769)]
 
 
 def _check_slices(torch, A, B, M, N, K, ta, tb, S, ws_fill=None):
