@@ -38,7 +38,8 @@ def _capture(torch, fn):
     (1024, 1024, 64, 0, 1, 1, 16),
     (256, 256, 256, 0, 0, 1, 16), (64, 120, 400, 0, 1, 1, 16),    # one-launch small kernel
     (300, 500, 1500, 1, 0, 1, (64, 192)), (500, 300, 700, 0, 1, 2, (192, 64)),   # 12 wavefronts
-    (1000, 300, 100, 0, 1, 1, (32, 128)), (2048, 768, 768, 0, 0, 1, (32, 256))])  # band kernel
+    (1000, 300, 100, 0, 1, 1, (32, 128)), (2048, 768, 768, 0, 0, 1, (32, 256)),  # band kernel
+    (96, 64, 40000, 0, 0, 1, 16), (64, 96, 36000, 1, 0, 2, 16)])  # wide one-read parts of op(B)
 def test_gemm_replays_equal_eager(torch_gpu, M, N, K, ta, tb, split, tile):
     torch = torch_gpu
     torch.manual_seed(M + N + K)

@@ -3,8 +3,9 @@
 An operand whose padded K is past the one-pass limit (column access: op(B) of an NN or TN GEMM,
 op(A) of a TN or TT GEMM, past 3072; row access past 4096) is read once: blocks hold a 32-column
 panel or an 8-row strip over a range of k in registers, and the blocks of a panel exchange their
-partial maxima through slots in the workspace that the call marks empty first (through the
-XCD's L2, or through memory for column-access operands of more than 32 parts). Checked against
+partial maxima through slots in the workspace that the call marks empty first, through the
+XCD's L2 (a column-access operand past K = 32768 takes parts twice as long, so that a panel
+never has more than 32). Checked against
 the oracle: every digit of both operands' panels, the exponents, the zero padding and the
 GEMM's bits, at S = 1..3, over every transpose, for K just past the limits, K with a partial
 last part, ragged panels and long K; the same with the wait bound set to zero (every block then
@@ -125,7 +126,8 @@ def test_one_read_slicing_repeated_calls_one_workspace(torch_gpu):
         assert np.array_equal(bits(C), want)
 
 
-@pytest.mark.parametrize("ta,tb,K", [(0, 0, 4000), (1, 0, 4000), (0, 1, 6000)])
+@pytest.mark.parametrize("ta,tb,K", [(0, 0, 4000), (1, 0, 4000), (0, 1, 6000), (1, 0, 40000),
+                                     (0, 0, 36000)])
 def test_one_read_slicing_batched(torch_gpu, ta, tb, K):
     torch = torch_gpu
     rng = np.random.default_rng(7 + ta + K)
