@@ -46,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "e5a5d5f2c9a7d4f02308b4f392d1cf1e9cd8a7623b545a8a76b3590168e8ced8"),
-    "slicing": (235627008, ("rg_slice.hip", "rg_internal.h"),
-                "4365ba3218111bc0089ac439b2a830e84ea00b5be37b078c5079c1d842c68b00"),
+                 "2b26057f523933aee64567e32d74b70616114d58eb15c74e68967f460a82fcf9"),
+    "slicing": (235602944, ("rg_slice.hip", "rg_internal.h"),
+                "fd8e1a3553aad65b0a0e21cb03d8f328848b1cbb2da52e45884f6e6299811758"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 

@@ -265,14 +265,19 @@ constexpr int PS_ROW_NPB = PS_WAVES * PS_ROW_NF4;
 // XCD at S = 3); with 64 parts they needed every slot at once and waited out their bound
 // (measured: 1024x1024x65536 NN), with 32 they did not.
 constexpr int PS_MAX_PARTS = 32;
-// Column-access operands that would need more parts (K past 32768) take parts twice as long:
-// PS_KPW_WIDE k panels per wavefront, so K up to 65536 is at most 32 parts, which still run
-// on one XCD and exchange through its L2 (the wide form: 173 registers, one block per compute
-// unit, 32 per XCD). Against 64 parts spread over every XCD exchanging through memory,
-// 1024x1024x65536 slicing took 0.259 -> 0.222 ms with both operands column-access (TN) and
-// 0.229 -> 0.224 ms with B alone (NN), on one box. Longer operands (column access past
-// K = 65536, row access past 131072) keep the two passes.
-constexpr int PS_KPW_WIDE = 8;
+// Column-access operands that would need more parts (K past 32768) take longer parts, the wide
+// form: PS_KPW_WIDE k panels per wavefront (2560 k per part), at most PS_MAX_PARTS_WIDE parts
+// per panel (K up to 66560). A wide block (205 registers at S = 3) fills its compute unit, so a
+// panel's parts take 26 of an XCD's 32 compute units and exchange through its L2; the other six
+// are slack, so that a kernel of another stream holding a few compute units of an XCD still
+// leaves room for a whole panel (with all 32 needed, the resident parts of such a panel would
+// wait out their bound and re-read K). Against 64 parts spread over every XCD exchanging through
+// memory, 1024x1024x65536 slicing took 0.259 -> 0.222 ms with both operands column-access (TN)
+// and 0.229 -> 0.224 ms with B alone (NN), on one box, with 2048 k per part (32 parts, no
+// slack); 2560 k per part measured the same on NN and 2-4% slower on TN and TT (3072 k: 3-8%).
+// Longer operands (column access past K = 66560, row access past 131072) keep the two passes.
+constexpr int PS_KPW_WIDE = 10;
+constexpr int PS_MAX_PARTS_WIDE = 26;
 // k panels per wavefront of a column-access operand's one read (0 for row access).
 __host__ __device__ inline int pslice_kpw(bool strided, int Kp) {
     if (!strided) return 0;
@@ -283,8 +288,8 @@ __host__ __device__ inline int pslice_parts(bool strided, int Kp) {
     return (Kp / PANEL_K + npb - 1) / npb;
 }
 __host__ __device__ inline bool pslice_route(bool strided, int Kp) {
-    return Kp > (strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K) &&
-           pslice_parts(strided, Kp) <= PS_MAX_PARTS;
+    const int cap = pslice_kpw(strided, Kp) == PS_KPW_WIDE ? PS_MAX_PARTS_WIDE : PS_MAX_PARTS;
+    return Kp > (strided ? ONEPASS_MAX_K_COLUMNS : ONEPASS_MAX_K) && pslice_parts(strided, Kp) <= cap;
 }
 // Polls of a block's wait for the other parts of its panel before it reads their k ranges
 // itself (rg_test_set_spin_limit sets it; 0: no exchange, every block reads its panel's whole K

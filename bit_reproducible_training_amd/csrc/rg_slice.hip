@@ -925,8 +925,9 @@ void launch_onepass_absmax(const SliceDesc& one, const SliceDesc& two, int S, hi
 // XCD's whole L2 while the launch's other blocks fill it with digits. A block whose parts ran on
 // another XCD can only see PM_EMPTY or this call's maxima (the slots were marked by an earlier
 // launch, whose writes the launch boundary made visible everywhere), so at worst it takes the
-// fallback: placement never changes a bit. KPW = PS_KPW_WIDE (K past 32768) doubles each
-// part's k range so that a panel still has at most 32 parts, which one XCD holds at once.
+// fallback: placement never changes a bit. KPW = PS_KPW_WIDE (K past 32768) makes each part
+// 2.5 times longer, so that a panel has at most 26 parts, which one XCD holds at once with room
+// to spare.
 // Eight slot words read past the L1 with one wait: a poll costs one round trip per eight parts
 // (the LM head's weight gradient, 8 parts: slicing 0.605 -> 0.595 ms against four per wait,
 // 0.65 ms with one).

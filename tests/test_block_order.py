@@ -123,7 +123,7 @@ def test_resident_blocks_share_panels(M, N, K, kw):
 # the LM head's (1571 column panels of 8 parts), a ragged batch, and the convolution weight
 # gradients of the widened benchmark (LeNet conv2: 10000 windows, 150 and 16 columns; ResNet-like
 # 100352 windows is past the one-read limit and keeps two passes), and column-access operands
-# past K = 32768, whose parts are twice as long (at most 32 per panel).
+# past K = 32768, whose parts are 2.5 times as long (at most 26 per panel).
 PSLICE_SHAPES = [
     (4096, 4096, 4096, 1, {}),
     (768, 768, 8192, 1, {"trans_a": True}),

@@ -4,8 +4,8 @@ An operand whose padded K is past the one-pass limit (column access: op(B) of an
 op(A) of a TN or TT GEMM, past 3072; row access past 4096) is read once: blocks hold a 32-column
 panel or an 8-row strip over a range of k in registers, and the blocks of a panel exchange their
 partial maxima through slots in the workspace that the call marks empty first, through the
-XCD's L2 (a column-access operand past K = 32768 takes parts twice as long, so that a panel
-never has more than 32). Checked against
+XCD's L2 (a column-access operand past K = 32768 takes parts 2.5 times as long, so that a
+panel never has more than 26; past K = 66560 it takes the two passes). Checked against
 the oracle: every digit of both operands' panels, the exponents, the zero padding and the
 GEMM's bits, at S = 1..3, over every transpose, for K just past the limits, K with a partial
 last part, ragged panels and long K; the same with the wait bound set to zero (every block then
@@ -24,11 +24,12 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 # Padded K from just past the column one-pass limit (3072) to several parts of 1024 k, and past
-# 32 such parts (K > 32768), where a column-access operand's parts are twice as long (2048 k:
-# at most 32 parts, on one XCD), including the boundary K = 32768 / 32769.
+# 32 such parts (K > 32768), where a column-access operand's parts are 2.5 times as long (2560 k:
+# at most 26 parts, on one XCD), including the boundaries K = 32768 / 32769 and 66560 / 66561
+# (26 wide parts / two passes for a column-access operand).
 SHAPES = [(64, 100, 3076), (33, 200, 4096), (100, 33, 5000), (130, 70, 8193), (32, 32, 3073),
           (70, 45, 4097), (24, 40, 12289), (9, 17, 20000), (40, 33, 40000), (20, 64, 65536),
-          (33, 40, 32768), (40, 20, 32769)]
+          (33, 40, 32768), (40, 20, 32769), (24, 40, 66560), (30, 20, 66561)]
 
 
 def _check_slices(torch, A, B, M, N, K, ta, tb, S, ws_fill=None):
