@@ -46,9 +46,9 @@ STEADY_STEPS = 50
 CSRC = os.path.join(REPO, "bit_reproducible_training_amd", "csrc")
 TRAFFIC = {
     "contract": (671606784, ("rg_contract.hip", "rg_internal.h"),
-                 "2b26057f523933aee64567e32d74b70616114d58eb15c74e68967f460a82fcf9"),
-    "slicing": (235602944, ("rg_slice.hip", "rg_internal.h"),
-                "fd8e1a3553aad65b0a0e21cb03d8f328848b1cbb2da52e45884f6e6299811758"),
+                 "aad6c405111935b53b5551a3876ec8e399399485b748e7b6e9606e5651ad0bf0"),
+    "slicing": (235601510, ("rg_slice.hip", "rg_internal.h"),
+                "a762ab26f759129cac13e138d0c181325da016b9360adccd2312f5678f9aaeb8"),
 }
 FIXTURE = os.path.join(REPO, "tests", "golden", "baseline_configs.json")
 

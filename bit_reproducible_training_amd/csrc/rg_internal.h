@@ -268,10 +268,11 @@ constexpr int PS_MAX_PARTS = 32;
 // Column-access operands that would need more parts (K past 32768) take longer parts, the wide
 // form: PS_KPW_WIDE k panels per wavefront (2560 k per part), at most PS_MAX_PARTS_WIDE parts
 // per panel (K up to 66560). A wide block (205 registers at S = 3) fills its compute unit, so a
-// panel's parts take 26 of an XCD's 32 compute units and exchange through its L2; the other six
-// are slack, so that a kernel of another stream holding a few compute units of an XCD still
-// leaves room for a whole panel (with all 32 needed, the resident parts of such a panel would
-// wait out their bound and re-read K). Against 64 parts spread over every XCD exchanging through
+// panel's parts take 26 of an XCD's 32 compute units and exchange through its L2; the rest is
+// slack for other streams' kernels: with a kernel of another stream holding two compute units
+// per XCD, 1024x1024x65536 slicing stayed at 0.23 ms, where 32 parts of 2048 k took 3.5 ms (every
+// panel's resident parts waiting out their bound, then re-reading K; same bits); with six held,
+// both took 3.5 ms. Against 64 parts spread over every XCD exchanging through
 // memory, 1024x1024x65536 slicing took 0.259 -> 0.222 ms with both operands column-access (TN)
 // and 0.229 -> 0.224 ms with B alone (NN), on one box, with 2048 k per part (32 parts, no
 // slack); 2560 k per part measured the same on NN and 2-4% slower on TN and TT (3072 k: 3-8%).
