@@ -167,3 +167,10 @@ def test_one_read_slicing_placement_hook_sees_the_routes():
     assert blocks(1024, 1024, 1024) == 0
     assert blocks(4096, 4096, 4096) > 0
     assert blocks(768, 768, 8192, trans_a=True) > 0
+    # both operands column-access (TN): the wide parts (2560 k, at most 26 per 32-column panel)
+    # reach K = 66560; one more k takes the two passes for both
+    assert blocks(64, 64, 66560, trans_a=True) == 2 * 8 * 26
+    assert blocks(64, 64, 66561, trans_a=True) == 0
+    # at K = 32768 the common parts (1024 k, 32 per panel), one k more the wide ones (13)
+    assert blocks(64, 64, 32768, trans_a=True) == 2 * 8 * 32
+    assert blocks(64, 64, 32769, trans_a=True) == 2 * 8 * 13
